@@ -1,0 +1,121 @@
+/*
+ * operatorlib C ABI — the stable, language-neutral boundary of the library.
+ *
+ * Every entry point takes device pointers that the caller owns, plain sizes
+ * and an opaque stream handle (a hipStream_t cast to void*, NULL = the null
+ * stream of the current device).  Each call validates its arguments before
+ * touching the HIP runtime, enqueues its kernels on `stream` and returns at
+ * once: it never synchronizes the device or the stream.
+ *
+ * Return value: a hipError_t value as int.  0 (hipSuccess) on success,
+ * 1 (hipErrorInvalidValue) for the argument errors listed per function
+ * (checked before any HIP call), otherwise the launch error reported by
+ * hipGetLastError().  Faults inside a kernel surface at the caller's next
+ * synchronization, as with any asynchronous HIP work.
+ *
+ * The C++ API in operatorlib/operators.h (the drop-in for the reference's
+ * include/operatorlib/operators.h:13-44) is a thin inline layer over these
+ * symbols; the PyTorch binding calls that C++ layer.
+ */
+#ifndef OPERATORLIB_OPERATORLIB_C_H_
+#define OPERATORLIB_OPERATORLIB_C_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* IEEE-754 binary16 bit pattern (the storage of __half / torch.float16). */
+typedef uint16_t operatorlib_half_t;
+
+/* Version of this ABI; bumped on any incompatible change. */
+#define OPERATORLIB_ABI_VERSION 1
+int operatorlib_abi_version(void);
+
+/* Human-readable text for a status returned by any entry point. */
+const char* operatorlib_status_string(int status);
+
+/*
+ * output[0] = sum(input[0..n)) as fp32.  Overwrites output (no prior zeroing
+ * needed).  Deterministic: the same input gives the same bits on every call.
+ * Errors: input/output NULL, n == 0.
+ * Replaces operatorlib::reduce_sum_f32, reference src/reduce.cu:54-69.
+ */
+int operatorlib_reduce_sum_f32(const float* input, float* output, size_t n,
+                               void* stream);
+
+/*
+ * Row-wise numerically stable softmax of a row-major [rows, cols] matrix.
+ * Errors: NULL pointer, rows <= 0, cols <= 0.
+ * Replaces operatorlib::softmax_f32, reference src/softmax.cu:182-202.
+ */
+int operatorlib_softmax_f32(const float* input, float* output, int rows,
+                            int cols, void* stream);
+
+/*
+ * output[c * rows + r] = input[r * cols + c] (out-of-place, bit-exact).
+ * Errors: NULL pointer, rows <= 0, cols <= 0.
+ * Replaces operatorlib::transpose_f32, reference src/transpose.cu:38-47.
+ */
+int operatorlib_transpose_f32(const float* input, float* output, int rows,
+                              int cols, void* stream);
+
+/*
+ * output[t, h] = input[t, h] * rsqrt(mean_h(input[t, :]^2) + epsilon)
+ *                * weight[h]  for a row-major [tokens, hidden] input.
+ * Errors: NULL pointer, tokens <= 0, hidden <= 0, epsilon <= 0 (or NaN).
+ * Replaces operatorlib::rmsnorm_f32, reference src/rmsnorm.cu:77-95.
+ */
+int operatorlib_rmsnorm_f32(const float* input, const float* weight,
+                            float* output, int tokens, int hidden,
+                            float epsilon, void* stream);
+
+/*
+ * Row-major C[m, n] = A[m, k] * B[k, n], fp32 in / fp32 out.
+ * Errors: NULL pointer, m/n/k <= 0.
+ * Replaces operatorlib::gemm_f32, reference src/gemm.cu:440-453.
+ */
+int operatorlib_gemm_f32(const float* a, const float* b, float* c, int m,
+                         int n, int k, void* stream);
+
+/*
+ * Row-major C[m, n] = A[m, k] * B[k, n]; fp16 A/B, fp32 accumulation and
+ * fp32 C.
+ * Errors: NULL pointer, m/n/k <= 0.
+ * Replaces operatorlib::gemm_f16, reference src/gemm.cu:455-479.
+ */
+int operatorlib_gemm_f16(const operatorlib_half_t* a,
+                         const operatorlib_half_t* b, float* c, int m, int n,
+                         int k, void* stream);
+
+/*
+ * output = softmax(Q K^T / sqrt(head_dim) [+ causal mask]) V for contiguous
+ * [batch, heads, sequence, head_dim] fp32 tensors; causal != 0 hides key j
+ * from query row i when j > i.
+ * Errors: NULL pointer, any size <= 0, head_dim > 128,
+ *         batch * heads > INT32_MAX.
+ * Replaces operatorlib::attention_f32, reference src/attention.cu:445-484.
+ */
+int operatorlib_attention_f32(const float* q, const float* k, const float* v,
+                              float* output, int batch, int heads,
+                              int sequence, int head_dim, int causal,
+                              void* stream);
+
+/*
+ * As operatorlib_attention_f32 with fp16 Q/K/V, fp32 scores, fp32
+ * online-softmax state and fp32 output.
+ * Replaces operatorlib::attention_f16, reference src/attention.cu:486-507.
+ */
+int operatorlib_attention_f16(const operatorlib_half_t* q,
+                              const operatorlib_half_t* k,
+                              const operatorlib_half_t* v, float* output,
+                              int batch, int heads, int sequence,
+                              int head_dim, int causal, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* OPERATORLIB_OPERATORLIB_C_H_ */

@@ -1,0 +1,468 @@
+// FlashAttention-style forward on the CDNA4 matrix cores.
+//   attention_f16: fp16 Q/K/V, v_mfma_f32_32x32x16_f16, fp32 scores and
+//                  online-softmax state, P rounded to fp16 for P.V, fp32 out
+//   attention_f32: fp32 Q/K/V, v_mfma_f32_32x32x2_f32, all fp32
+//
+// Reference: operatorlib::attention_f16 / attention_f32
+// (src/attention.cu:445-507). Same maths: per (batch, head),
+//   O = softmax(Q K^T / sqrt(D), keys j > row i hidden when causal) V,
+// computed with the online recurrence m' = max(m, x), a = e^(m - m'),
+// l' = a l + sum e^(x - m'), O' = a O + e^(x - m') V (src/attention.cu:116-134,
+// :296-349) so no S x S matrix is ever stored. As in the reference FP16
+// path, P is rounded to fp16 before the P.V product and the row sum uses the
+// unrounded fp32 values (src/attention.cu:313-320).
+//
+// MI355X design, per 256-thread workgroup (4 wavefronts x 32 query rows):
+//   * scores are computed transposed, S^T = K Q^T, so lane l of a wavefront
+//     owns query row (l % 32): its row max / row sum need only the lane's
+//     own registers plus one exchange with lane l ^ 32;
+//   * the S^T accumulator registers are exactly the B operand of the next
+//     MFMA, O^T += V^T P^T, so P never leaves registers; V is stored
+//     transposed in LDS with its keys permuted to match that register
+//     layout (fp16), or read row-wise straight from LDS (fp32);
+//   * K / V tiles (64 keys fp16, 32 keys fp32) are double-buffered in LDS;
+//     global loads of tile t+1 overlap the MFMAs of tile t;
+//   * exp is exp2 on v_exp_f32 with log2(e)/sqrt(D) folded into one FMA;
+//     the O rescale is skipped when no row max in the wavefront moved;
+//   * causal: key tiles beyond the workgroup's last row are never loaded,
+//     wavefronts skip tiles beyond their own rows, masks are applied only on
+//     diagonal / ragged tiles; workgroups are issued heaviest-first, and
+//     all workgroups of one head share an XCD (and its L2).
+// Head dims are padded to a multiple of 32 with zeros (any 1 <= D <= 128).
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+
+#include "common.hpp"
+#include "operatorlib/operatorlib_c.h"
+#include "validate.hpp"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / opl::kWaveSize;
+constexpr int kRowsPerWave = 32;
+constexpr int kBlockRows = kWaves * kRowsPerWave;  // 128
+
+template <typename T>
+struct AttnPrec;
+
+template <>
+struct AttnPrec<_Float16> {
+  using Chunk = half8;                // 16 bytes of Q / K / V
+  static constexpr int kKeyTiles = 2;  // 32-key MFMA tiles per K/V tile
+  __device__ __forceinline__ static void mma(floatx16& acc, const Chunk& a,
+                                             const Chunk& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+  }
+};
+
+template <>
+struct AttnPrec<float> {
+  using Chunk = float4v;
+  static constexpr int kKeyTiles = 1;
+  __device__ __forceinline__ static void mma(floatx16& acc, const Chunk& a,
+                                             const Chunk& b) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc, 0, 0, 0);
+  }
+};
+
+template <typename T, int NDT>
+struct AttnLayout {
+  static constexpr int E = 16 / sizeof(T);          // elements per chunk
+  static constexpr int kDP = 32 * NDT;              // padded head dim
+  static constexpr int kKeys = 32 * AttnPrec<T>::kKeyTiles;  // keys per tile
+  static constexpr int kDChunks = kDP / E;          // chunks per K/V row
+  static constexpr int kChunkPairs = kDChunks / 2;  // MFMA k-steps over d
+  // K tile: [kKeys][kDP], row pitch padded by 16 B.
+  static constexpr int kKPitch = kDP * sizeof(T) + 16;
+  static constexpr int kKBytes = kKeys * kKPitch;
+  // V tile: fp16 -> transposed [kDP][kKeys] (keys permuted), pitch + 16 B;
+  //         fp32 -> row-major [kKeys][kDP + 8] (rows r and r+4 land 32
+  //         banks apart for the column reads).
+  static constexpr int kVPitch = sizeof(T) == 2 ? kKeys * 2 + 16
+                                                : (kDP + 8) * 4;
+  static constexpr int kVBytes = sizeof(T) == 2 ? kDP * kVPitch
+                                                : kKeys * kVPitch;
+  static constexpr int kStageBytes = kKBytes + kVBytes;
+  static constexpr int kLdsBytes = 2 * kStageBytes;
+};
+
+// Position of key r (0..15) inside its 16-key group of the transposed fp16
+// V tile: the two middle quads swap, so that lane half h finds the 8 keys
+// of its P^T operand (keys 4h..4h+3 and 8+4h..8+4h+3) contiguous.
+__device__ __forceinline__ int vt_pos(int r) {
+  return 8 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3);
+}
+
+template <typename T, bool kVector>
+__device__ __forceinline__ typename AttnPrec<T>::Chunk load_chunk(
+    const T* base, int row, int rows, int col, int cols, int ld) {
+  using Chunk = typename AttnPrec<T>::Chunk;
+  constexpr int E = 16 / sizeof(T);
+  Chunk v;
+  if constexpr (kVector) {
+    if (row < rows && col < cols) {
+      v = *reinterpret_cast<const Chunk*>(
+          base + static_cast<std::size_t>(row) * ld + col);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[e] = T(0);
+    }
+  } else {
+    const T* p = base + static_cast<std::size_t>(row) * ld;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      v[e] = (row < rows && col + e < cols) ? p[col + e] : T(0);
+  }
+  return v;
+}
+
+// Global -> register staging of one K/V tile, then register -> LDS.
+template <typename T, int NDT, bool kVector>
+struct KvStager {
+  using L = AttnLayout<T, NDT>;
+  using Chunk = typename AttnPrec<T>::Chunk;
+  static constexpr int E = L::E;
+  static constexpr int kKItems = L::kKeys * L::kDChunks;             // chunks
+  static constexpr int kKPerThread = (kKItems + kThreads - 1) / kThreads;
+  // fp16 V: E x E blocks (E keys x E dims); fp32 V: plain chunks like K.
+  static constexpr int kVItems =
+      sizeof(T) == 2 ? (L::kKeys / E) * (L::kDP / E) : kKItems;
+  static constexpr int kVPerThread = (kVItems + kThreads - 1) / kThreads;
+  static constexpr int kVRows = sizeof(T) == 2 ? E : 1;
+
+  Chunk k[kKPerThread];
+  Chunk v[kVPerThread][kVRows];
+
+  __device__ __forceinline__ void load(const T* kbase, const T* vbase,
+                                       int key0, int S, int D) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kKPerThread; ++i) {
+      const int q = tid + kThreads * i;
+      if (q < kKItems) {
+        const int key = q / L::kDChunks;
+        const int c = q % L::kDChunks;
+        k[i] = load_chunk<T, kVector>(kbase, key0 + key, S, c * E, D, D);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kVPerThread; ++i) {
+      const int q = tid + kThreads * i;
+      if (q < kVItems) {
+        if constexpr (sizeof(T) == 2) {
+          const int kb = q / (L::kDP / E);  // key block of E keys
+          const int c = q % (L::kDP / E);   // dim chunk
+#pragma unroll
+          for (int r = 0; r < E; ++r)
+            v[i][r] = load_chunk<T, kVector>(vbase, key0 + kb * E + r, S,
+                                             c * E, D, D);
+        } else {
+          const int key = q / L::kDChunks;
+          const int c = q % L::kDChunks;
+          v[i][0] = load_chunk<T, kVector>(vbase, key0 + key, S, c * E, D, D);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(unsigned char* stage) const {
+    const int tid = threadIdx.x;
+    unsigned char* sk = stage;
+    unsigned char* sv = stage + L::kKBytes;
+#pragma unroll
+    for (int i = 0; i < kKPerThread; ++i) {
+      const int q = tid + kThreads * i;
+      if (q < kKItems) {
+        const int key = q / L::kDChunks;
+        const int c = q % L::kDChunks;
+        *reinterpret_cast<Chunk*>(sk + key * L::kKPitch + c * 16) = k[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kVPerThread; ++i) {
+      const int q = tid + kThreads * i;
+      if (q < kVItems) {
+        if constexpr (sizeof(T) == 2) {
+          const int kb = q / (L::kDP / E);
+          const int c = q % (L::kDP / E);
+          // Keys kb*8 .. kb*8+7 sit in 16-key group kb/2 at positions
+          // vt_pos(8*(kb%2) + r): two runs of 4 contiguous keys.
+          const int group_byte = (kb >> 1) * 32;
+          const int p0 = vt_pos(8 * (kb & 1)) * 2;
+          const int p1 = vt_pos(8 * (kb & 1) + 4) * 2;
+#pragma unroll
+          for (int dd = 0; dd < E; ++dd) {
+            half4 lo, hi;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              lo[r] = v[i][r][dd];
+              hi[r] = v[i][r + 4][dd];
+            }
+            unsigned char* row = sv + (c * E + dd) * L::kVPitch + group_byte;
+            *reinterpret_cast<half4*>(row + p0) = lo;
+            *reinterpret_cast<half4*>(row + p1) = hi;
+          }
+        } else {
+          const int key = q / L::kDChunks;
+          const int c = q % L::kDChunks;
+          *reinterpret_cast<Chunk*>(sv + key * L::kVPitch + c * 16) = v[i][0];
+        }
+      }
+    }
+  }
+};
+
+template <typename T, int NDT, bool kVector>
+__global__ __launch_bounds__(kThreads) void attention_mfma_kernel(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+    float* __restrict__ O, int BH, int S, int D, int causal,
+    float score_scale_log2) {
+  using L = AttnLayout<T, NDT>;
+  using Pr = AttnPrec<T>;
+  using Chunk = typename Pr::Chunk;
+  constexpr int NKB = Pr::kKeyTiles;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::kLdsBytes];
+
+  // Heaviest query blocks first; all blocks of one head map to one XCD
+  // (launch index modulo 8) whenever BH is a multiple of 8.
+  const int q_blocks = (S + kBlockRows - 1) / kBlockRows;
+  const int qb = q_blocks - 1 - static_cast<int>(blockIdx.x / BH);
+  const int bh = static_cast<int>(blockIdx.x % BH);
+  const int q0 = qb * kBlockRows;
+
+  const int lane = threadIdx.x % opl::kWaveSize;
+  const int wave = threadIdx.x / opl::kWaveSize;
+  const int half = lane / 32;
+  const int l32 = lane % 32;
+  const int wave_row0 = q0 + wave * kRowsPerWave;
+  const int my_row = wave_row0 + l32;
+
+  const std::size_t head = static_cast<std::size_t>(bh) * S * D;
+  const T* qh = Q + head;
+  const T* kh = K + head;
+  const T* vh = V + head;
+
+  // Q^T operand: lane (row, half) holds chunk (2c + half) of its row.
+  Chunk qf[L::kChunkPairs];
+#pragma unroll
+  for (int c = 0; c < L::kChunkPairs; ++c)
+    qf[c] = load_chunk<T, kVector>(qh, my_row, S, (2 * c + half) * L::E, D, D);
+
+  floatx16 o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
+  float row_max = -FLT_MAX;  // finite sentinel: e^(sentinel - m) == 0
+  float row_sum = 0.0f;      // this lane's half of the row sum
+
+  const int visible_end = causal ? min(S, q0 + kBlockRows) : S;
+  const int tiles = (visible_end + L::kKeys - 1) / L::kKeys;
+
+  KvStager<T, NDT, kVector> stager;
+  stager.load(kh, vh, 0, S, D);
+  stager.store(lds);
+  __syncthreads();
+
+  for (int tile = 0; tile < tiles; ++tile) {
+    const unsigned char* stage = lds + (tile & 1) * L::kStageBytes;
+    const int key0 = tile * L::kKeys;
+    if (tile + 1 < tiles) stager.load(kh, vh, key0 + L::kKeys, S, D);
+
+    const bool wave_active = !causal || key0 <= wave_row0 + kRowsPerWave - 1;
+    if (wave_active) {
+      // ---- S^T = K Q^T for NKB 32-key tiles --------------------------------
+      floatx16 s[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
+        const unsigned char* krow = stage + (32 * kb + l32) * L::kKPitch;
+#pragma unroll
+        for (int c = 0; c < L::kChunkPairs; ++c) {
+          const Chunk a =
+              *reinterpret_cast<const Chunk*>(krow + (2 * c + half) * 16);
+          Pr::mma(s[kb], a, qf[c]);
+        }
+      }
+      // ---- online softmax (log2 domain) --------------------------------------
+      const bool needs_mask =
+          key0 + L::kKeys > S ||
+          (causal && key0 + L::kKeys - 1 > wave_row0);
+      float tile_max = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float x = s[kb][e] * score_scale_log2;
+          if (needs_mask) {
+            const int key = key0 + 32 * kb + 8 * (e / 4) + 4 * half + (e % 4);
+            if (key >= S || (causal && key > my_row)) x = -INFINITY;
+          }
+          s[kb][e] = x;
+          tile_max = fmaxf(tile_max, x);
+        }
+      }
+      tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+      const float new_max = fmaxf(row_max, tile_max);
+      const float alpha = opl::fast_exp2(row_max - new_max);
+      row_max = new_max;
+      float psum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float p = opl::fast_exp2(s[kb][e] - new_max);
+          s[kb][e] = p;
+          psum += p;
+        }
+      }
+      row_sum = row_sum * alpha + psum;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+      }
+      // ---- O^T += V^T P^T -----------------------------------------------------
+      const unsigned char* vtile = stage + L::kKBytes;
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            half8 pb;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              pb[e] = static_cast<_Float16>(s[kb][8 * u + e]);
+            const int group_byte = (2 * kb + u) * 32 + 16 * half;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+              const half8 a = *reinterpret_cast<const half8*>(
+                  vtile + (32 * dt + l32) * L::kVPitch + group_byte);
+              o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0,
+                                                              0, 0);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = 8 * (e / 4) + 4 * half + (e % 4);
+          const float* vrow =
+              reinterpret_cast<const float*>(vtile + key * L::kVPitch);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                vrow[32 * dt + l32], s[0][e], o[dt], 0, 0, 0);
+        }
+      }
+    }
+
+    if (tile + 1 < tiles) stager.store(lds + ((tile + 1) & 1) * L::kStageBytes);
+    __syncthreads();
+  }
+
+  // ---- normalise and store: lane holds O^T[d][row] for d = 32dt + 8(e/4) +
+  // 4*half + e%4, i.e. four runs of 4 consecutive dims per tile ------------
+  const float total = row_sum + __shfl_xor(row_sum, 32);
+  const float inv = 1.0f / total;
+  if (my_row < S) {
+    float* orow = O + head + static_cast<std::size_t>(my_row) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * dt + 8 * g + 4 * half;
+        if constexpr (kVector) {
+          if (d0 < D)
+            *reinterpret_cast<float4*>(orow + d0) =
+                make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv,
+                            o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (d0 + r < D) orow[d0 + r] = o[dt][4 * g + r] * inv;
+        }
+      }
+    }
+  }
+}
+
+template <typename T, int NDT>
+void launch_attention(const T* q, const T* k, const T* v, float* out, int bh,
+                      int s, int d, int causal, bool vector_ok,
+                      hipStream_t stream) {
+  const int q_blocks = (s + kBlockRows - 1) / kBlockRows;
+  const long long blocks = static_cast<long long>(q_blocks) * bh;
+  const float scale = 1.4426950408889634f / sqrtf(static_cast<float>(d));
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+  if (vector_ok)
+    attention_mfma_kernel<T, NDT, true><<<grid, block, 0, stream>>>(
+        q, k, v, out, bh, s, d, causal, scale);
+  else
+    attention_mfma_kernel<T, NDT, false><<<grid, block, 0, stream>>>(
+        q, k, v, out, bh, s, d, causal, scale);
+}
+
+template <typename T>
+int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
+                    int heads, int sequence, int head_dim, int causal,
+                    void* stream_handle) {
+  if (!opl::attention_args_ok(q, k, v, out, batch, heads, sequence, head_dim))
+    return hipErrorInvalidValue;
+  const int bh = batch * heads;
+  const long long blocks =
+      static_cast<long long>((sequence + kBlockRows - 1) / kBlockRows) * bh;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  constexpr int E = 16 / sizeof(T);
+  const bool vector_ok = head_dim % E == 0 && opl::aligned16(q) &&
+                         opl::aligned16(k) && opl::aligned16(v) &&
+                         opl::aligned16(out);
+  hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+  const int c = causal ? 1 : 0;
+  switch ((head_dim + 31) / 32) {
+    case 1: launch_attention<T, 1>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream); break;
+    case 2: launch_attention<T, 2>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream); break;
+    case 3: launch_attention<T, 3>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream); break;
+    default: launch_attention<T, 4>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int operatorlib_attention_f32(const float* q, const float* k,
+                                         const float* v, float* output,
+                                         int batch, int heads, int sequence,
+                                         int head_dim, int causal,
+                                         void* stream_handle) {
+  return attention_entry<float>(q, k, v, output, batch, heads, sequence,
+                                head_dim, causal, stream_handle);
+}
+
+extern "C" int operatorlib_attention_f16(const operatorlib_half_t* q,
+                                         const operatorlib_half_t* k,
+                                         const operatorlib_half_t* v,
+                                         float* output, int batch, int heads,
+                                         int sequence, int head_dim,
+                                         int causal, void* stream_handle) {
+  return attention_entry<_Float16>(reinterpret_cast<const _Float16*>(q),
+                                   reinterpret_cast<const _Float16*>(k),
+                                   reinterpret_cast<const _Float16*>(v),
+                                   output, batch, heads, sequence, head_dim,
+                                   causal, stream_handle);
+}

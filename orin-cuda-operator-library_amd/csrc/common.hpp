@@ -1,0 +1,154 @@
+#pragma once
+// Device-side building blocks shared by the operatorlib kernels (gfx950,
+// 64-lane wavefronts).
+//
+// Cross-lane reductions use the CDNA data-parallel primitives instead of
+// generic shuffles: DPP quad permutes and row mirrors combine lanes inside a
+// 16-lane row, ds_swizzle (bit-mask mode) combines the two rows of each
+// 32-lane half, and two v_readlane_b32 combine the halves into a wave-uniform
+// scalar. Every step is a full butterfly, so all lanes see identical bits and
+// the result is independent of scheduling (bitwise deterministic).
+//
+// The reductions require all 64 lanes to be active: callers pad inactive
+// elements with the operation's identity instead of branching around the
+// call.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace opl {
+
+constexpr int kWaveSize = 64;
+
+// DPP control words (GCN/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
+constexpr int kDppRowMirror = 0x140;     // lane i <-> 15-i within 16 lanes
+// ds_swizzle bit-mask mode: and=0x1f, or=0, xor=0x10 -> lane ^ 16.
+constexpr int kSwizzleXor16 = 0x401F;
+
+template <int Ctrl>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, Ctrl, 0xF, 0xF, false);
+}
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, dpp_i32<Ctrl>(__builtin_bit_cast(int, v)));
+}
+
+template <int Ctrl>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const std::uint64_t bits = __builtin_bit_cast(std::uint64_t, v);
+  const int lo = dpp_i32<Ctrl>(static_cast<int>(bits & 0xffffffffu));
+  const int hi = dpp_i32<Ctrl>(static_cast<int>(bits >> 32));
+  const std::uint64_t out = (static_cast<std::uint64_t>(
+                                 static_cast<std::uint32_t>(hi))
+                             << 32) |
+                            static_cast<std::uint32_t>(lo);
+  return __builtin_bit_cast(double, out);
+}
+
+__device__ __forceinline__ float swizzle_xor16_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v),
+                                         kSwizzleXor16));
+}
+
+__device__ __forceinline__ double swizzle_xor16_f64(double v) {
+  const std::uint64_t bits = __builtin_bit_cast(std::uint64_t, v);
+  const int lo = __builtin_amdgcn_ds_swizzle(
+      static_cast<int>(bits & 0xffffffffu), kSwizzleXor16);
+  const int hi =
+      __builtin_amdgcn_ds_swizzle(static_cast<int>(bits >> 32), kSwizzleXor16);
+  const std::uint64_t out = (static_cast<std::uint64_t>(
+                                 static_cast<std::uint32_t>(hi))
+                             << 32) |
+                            static_cast<std::uint32_t>(lo);
+  return __builtin_bit_cast(double, out);
+}
+
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const std::uint64_t bits = __builtin_bit_cast(std::uint64_t, v);
+  const std::uint32_t lo = static_cast<std::uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(bits & 0xffffffffu), lane));
+  const std::uint32_t hi = static_cast<std::uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(bits >> 32), lane));
+  return __builtin_bit_cast(double,
+                            (static_cast<std::uint64_t>(hi) << 32) | lo);
+}
+
+struct SumOp {
+  template <typename T>
+  __device__ __forceinline__ static T apply(T a, T b) {
+    return a + b;
+  }
+};
+
+struct MaxOp {
+  __device__ __forceinline__ static float apply(float a, float b) {
+    return fmaxf(a, b);
+  }
+};
+
+// Wave-wide all-reduce; every lane receives the same (uniform) value.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v) {
+  v = Op::apply(v, dpp_f32<kDppQuadXor1>(v));
+  v = Op::apply(v, dpp_f32<kDppQuadXor2>(v));
+  v = Op::apply(v, dpp_f32<kDppRowHalfMirror>(v));
+  v = Op::apply(v, dpp_f32<kDppRowMirror>(v));
+  v = Op::apply(v, swizzle_xor16_f32(v));
+  return Op::apply(readlane_f32(v, 0), readlane_f32(v, 32));
+}
+
+__device__ __forceinline__ double wave_reduce_sum_f64(double v) {
+  v += dpp_f64<kDppQuadXor1>(v);
+  v += dpp_f64<kDppQuadXor2>(v);
+  v += dpp_f64<kDppRowHalfMirror>(v);
+  v += dpp_f64<kDppRowMirror>(v);
+  v += swizzle_xor16_f64(v);
+  return readlane_f64(v, 0) + readlane_f64(v, 32);
+}
+
+// Block-wide all-reduce over `Waves` wavefronts through a small LDS array
+// (`slots` must hold `Waves` floats and must not be reused by the caller
+// until after the next __syncthreads()). Partial results are combined in
+// wave order, so the result is deterministic.
+template <class Op, int Waves>
+__device__ __forceinline__ float block_reduce(float v, float* slots) {
+  v = wave_reduce<Op>(v);
+  if constexpr (Waves == 1) {
+    return v;
+  } else {
+    const int wave = threadIdx.x / kWaveSize;
+    if ((threadIdx.x % kWaveSize) == 0) slots[wave] = v;
+    __syncthreads();
+    float r = slots[0];
+#pragma unroll
+    for (int w = 1; w < Waves; ++w) r = Op::apply(r, slots[w]);
+    return r;
+  }
+}
+
+// 2^x on the hardware transcendental unit (v_exp_f32). Callers fold log2(e)
+// into their arguments so that exp(x) costs one FMA plus one v_exp_f32.
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Alignment test for the 16-byte vector paths.
+__host__ __device__ inline bool aligned16(const void* p) {
+  return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0;
+}
+
+}  // namespace opl

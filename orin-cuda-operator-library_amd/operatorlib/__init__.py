@@ -1,0 +1,102 @@
+"""operatorlib for MI355X — Python entry points.
+
+* ``load_operatorlib()`` registers ``torch.ops.operatorlib.{reduce_sum,
+  softmax, transpose, rmsnorm, gemm, attention}`` from the prebuilt in-tree
+  extension. It mirrors the reference's ``python/load_extension.py:17-36``
+  (which JIT-compiled CUDA sources); here the HIP build happens ahead of time
+  (``build()``) and loading never compiles anything.
+* ``clib()`` returns the ``ctypes`` handle of ``liboperatorlib.so`` with the
+  C ABI of ``include/operatorlib/operatorlib_c.h`` typed, for callers that
+  want the library without the torch layer.
+
+Both raise if the native library has not been built: there is no fallback
+implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+from . import _build
+
+LIB_DIR = _build.LIB_DIR
+LIBRARY_PATH = _build.LIBRARY
+TORCH_EXT_PATH = _build.TORCH_EXT
+
+__all__ = ["build", "load_operatorlib", "clib", "LIBRARY_PATH", "TORCH_EXT_PATH",
+           "C_SYMBOLS", "HIP_SUCCESS", "HIP_ERROR_INVALID_VALUE"]
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+
+_c = ctypes
+# name -> (restype, argtypes); mirrors include/operatorlib/operatorlib_c.h
+C_SYMBOLS = {
+    "operatorlib_abi_version": (_c.c_int, []),
+    "operatorlib_status_string": (_c.c_char_p, [_c.c_int]),
+    "operatorlib_reduce_sum_f32": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "operatorlib_softmax_f32": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_void_p]),
+    "operatorlib_transpose_f32": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_void_p]),
+    "operatorlib_rmsnorm_f32": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int,
+                                           _c.c_float, _c.c_void_p]),
+    "operatorlib_gemm_f32": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int,
+                                        _c.c_int, _c.c_void_p]),
+    "operatorlib_gemm_f16": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int,
+                                        _c.c_int, _c.c_void_p]),
+    "operatorlib_attention_f32": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_void_p,
+                                             _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                                             _c.c_void_p]),
+    "operatorlib_attention_f16": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_void_p,
+                                             _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                                             _c.c_void_p]),
+}
+
+_clib = None
+_torch_loaded = False
+
+
+def build(verbose: bool = False, torch_binding: bool = True, smoke: bool = True) -> None:
+    """Compile every native artefact for gfx950 (see ``_build``)."""
+    _build.build(verbose=verbose, torch_binding=torch_binding, smoke=smoke)
+
+
+def _require(path: Path) -> None:
+    if not path.exists():
+        raise RuntimeError(
+            f"operatorlib native library missing: {path}. Build it first "
+            "(python -c 'import __graft_entry__ as g; g.build()').")
+
+
+def clib() -> ctypes.CDLL:
+    """Load ``liboperatorlib.so`` and type its C ABI."""
+    global _clib
+    if _clib is None:
+        _require(LIBRARY_PATH)
+        try:
+            # Share the HIP runtime torch already loaded (same SONAME) when
+            # torch is importable, so both use one runtime instance.
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        lib = ctypes.CDLL(str(LIBRARY_PATH), mode=ctypes.RTLD_GLOBAL)
+        for name, (restype, argtypes) in C_SYMBOLS.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _clib = lib
+    return _clib
+
+
+def load_operatorlib(verbose: bool = False) -> None:
+    """Register ``torch.ops.operatorlib.*`` (reference: load_extension.py:17)."""
+    global _torch_loaded
+    if _torch_loaded:
+        return
+    import torch
+    _require(TORCH_EXT_PATH)
+    clib()  # the extension links liboperatorlib.so; load it first, same runtime
+    torch.ops.load_library(str(TORCH_EXT_PATH))
+    if verbose:
+        print(f"loaded {TORCH_EXT_PATH}")
+    _torch_loaded = True

@@ -1,0 +1,284 @@
+"""GPU parity tests: HIP kernels (through the C ABI) against the CPU oracle.
+
+Tolerances are the BASELINE contract, written here:
+  transpose                bit-exact
+  reduce                   |y - ref| <= 1e-5 |ref|           (ref fp64)
+  softmax, rmsnorm         elementwise max |y-ref|/|ref| over |ref| >= 1e-30,
+                           and normwise ||y-ref||/||ref||, each <= 1e-5
+  gemm_f32                 ||C - ref||_F / ||ref||_F <= 1e-4
+  gemm_f16, attention_f16  max |y - ref| <= 2e-3, ref fp64 on fp16-rounded
+                           inputs
+  attention_f32            |y - ref| <= 1e-4 + 1e-4 |ref| (the reference's
+                           tests/attention_smoke.cu:108 bound)
+Small shapes hit every dispatch path of the reference (its smoke-test shape
+matrix) and of this library; BASELINE shapes run at full size, checked in
+full where the oracle is fast and on seeded row samples (always including
+the first and last rows) where it is not.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import pins
+from gpu_util import HipOps
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip(lib):
+    return HipOps(lib)
+
+
+def rel_errors(y: np.ndarray, ref: np.ndarray) -> tuple[float, float]:
+    mask = np.abs(ref) >= 1e-30
+    elem = float(np.max(np.abs(y[mask] - ref[mask]) / np.abs(ref[mask]))) if mask.any() else 0.0
+    norm = float(np.linalg.norm((y - ref).ravel()) / max(np.linalg.norm(ref.ravel()), 1e-300))
+    return elem, norm
+
+
+def sample_rows(n: int, count: int, seed: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    rows = set(rng.choice(n, size=min(count, n), replace=False).tolist())
+    rows.update({0, n - 1})
+    return np.array(sorted(rows), dtype=np.int32)
+
+
+# ------------------------------------------------------------------------ reduce
+
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 1000, 1023, 4097, 1_000_003, 16_777_216])
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_reduce_matches_oracle(hip, n, offset):
+    x = oracle.uniform(100 + n, n)
+    ref = oracle.reduce_sum(x)
+    y = hip.reduce_sum(x, offset)
+    assert abs(y - ref) <= 1e-5 * abs(ref)
+    # design claim: fp64 accumulation -> within one fp32 rounding of ref
+    assert abs(y - ref) <= float(np.spacing(np.float32(abs(ref))))
+
+
+def test_reduce_pins_and_determinism(hip):
+    pins.pin_reduce(hip.reduce_sum, tol_rel=1e-7)
+    x = oracle.uniform(7, 16_777_216)
+    a, b = hip.reduce_sum(x), hip.reduce_sum(x)
+    assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)
+
+
+def test_reduce_two_streams(lib):
+    """Concurrent reduces on two streams use separate scratch."""
+    from gpu_util import ptr, stream_handle, to_device
+    xs = [oracle.uniform(40 + i, 3_000_000) for i in range(2)]
+    ds = [to_device(x) for x in xs]
+    outs = [torch.empty(1, device="cuda") for _ in xs]
+    streams = [torch.cuda.Stream() for _ in xs]
+    torch.cuda.synchronize()
+    for _ in range(20):
+        for d, o, s in zip(ds, outs, streams):
+            assert lib.operatorlib_reduce_sum_f32(ptr(d), ptr(o), d.numel(),
+                                                  stream_handle(s)) == 0
+    torch.cuda.synchronize()
+    for x, o in zip(xs, outs):
+        ref = oracle.reduce_sum(x)
+        assert abs(o.item() - ref) <= 1e-5 * abs(ref)
+
+
+# ----------------------------------------------------------------------- softmax
+
+SOFTMAX_SHAPES = [(19, 128), (17, 1024), (17, 1003), (5, 1), (3, 7), (1, 4096),
+                  (7, 4100), (3, 9000), (2, 32768), (2, 40000), (3, 33333),
+                  (4096, 1024), (4097, 1023)]
+
+
+@pytest.mark.parametrize("shape", SOFTMAX_SHAPES)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_softmax_matches_oracle(hip, shape, offset):
+    x = oracle.normal(200 + shape[1], shape, 0.0, 3.0)
+    ref = oracle.softmax(x)
+    y = hip.softmax(x, offset)
+    elem, norm = rel_errors(y, ref)
+    assert elem <= 1e-5 and norm <= 1e-5, (elem, norm)
+
+
+@pytest.mark.parametrize("shape", [(17, 1003), (19, 128), (4, 5000), (2, 40000)])
+def test_softmax_extreme_scale(hip, shape):
+    # tests/core_ops_smoke.cu:174: uniform(-1000, 1000) rows; the reference's
+    # max-abs 2e-5 and row-sum 2e-5 bounds
+    x = oracle.uniform(300, shape, -1000.0, 1000.0)
+    ref = oracle.softmax(x)
+    y = hip.softmax(x)
+    assert np.max(np.abs(y - ref)) <= 2e-5
+    assert np.max(np.abs(y.sum(-1) - 1.0)) <= 2e-5
+
+
+def test_softmax_pins(hip):
+    pins.pin_softmax(hip.softmax, tol=2e-7)
+
+
+# --------------------------------------------------------------------- transpose
+
+TRANSPOSE_SHAPES = [(37, 65), (64, 96), (65, 37), (1, 1), (1, 1000), (1000, 1),
+                    (64, 64), (129, 257), (4096, 4096), (4095, 4097)]
+
+
+@pytest.mark.parametrize("shape", TRANSPOSE_SHAPES)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_transpose_bit_exact(hip, shape, offset):
+    x = oracle.uniform(400 + shape[0], shape)
+    y = hip.transpose(x, offset)
+    ref = oracle.transpose(x)
+    assert y.view(np.uint32).tobytes() == ref.view(np.uint32).tobytes()
+
+
+def test_transpose_pins(hip):
+    pins.pin_transpose(hip.transpose)
+
+
+def test_transpose_involution_full_size(hip):
+    x = oracle.uniform(401, (4095, 4097))
+    assert np.array_equal(hip.transpose(hip.transpose(x).astype(np.float32)), x)
+
+
+# ----------------------------------------------------------------------- rmsnorm
+
+RMSNORM_CASES = [((32, 4096), 1e-5), ((17, 1003), 1e-5), ((21, 1024), 1e-5),
+                 ((5, 1003), 1e-5), ((3, 1), 1e-5), ((4, 10000), 1e-6),
+                 ((2, 32768), 1e-6), ((2, 40001), 1e-6), ((2048, 4096), 1e-6),
+                 ((2047, 4095), 1e-6)]
+
+
+@pytest.mark.parametrize("shape,eps", RMSNORM_CASES)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_rmsnorm_matches_oracle(hip, shape, eps, offset):
+    x = oracle.normal(500 + shape[1], shape)
+    w = oracle.uniform(501, shape[1], 0.5, 1.5)
+    ref = oracle.rmsnorm(x, w, eps)
+    y = hip.rmsnorm(x, w, eps, offset)
+    elem, norm = rel_errors(y, ref)
+    assert elem <= 1e-5 and norm <= 1e-5, (elem, norm)
+
+
+def test_rmsnorm_pins(hip):
+    pins.pin_rmsnorm(hip.rmsnorm, tol=3e-7)
+
+
+# -------------------------------------------------------------------------- gemm
+
+GEMM_SMALL = [(1, 256, 64), (16, 128, 64), (128, 64, 32), (37, 65, 71), (7, 37, 23),
+              (128, 128, 32), (16, 128, 32), (32, 32, 32), (17, 19, 23),
+              (256, 256, 256), (300, 520, 200), (513, 129, 1000)]
+
+
+@pytest.mark.parametrize("mnk", GEMM_SMALL)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_gemm_f32_small(hip, mnk, offset):
+    m, n, k = mnk
+    a = oracle.uniform(600 + m, (m, k))
+    b = oracle.uniform(601 + n, (k, n))
+    ref = oracle.gemm(a, b)
+    y = hip.gemm_f32(a, b, offset)
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
+    # the reference smoke bound (tests/gemm_smoke.cu:76), elementwise
+    assert np.all(np.abs(y - ref) <= 1e-3 + 1e-3 * np.abs(ref))
+
+
+@pytest.mark.parametrize("mnk", GEMM_SMALL)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_gemm_f16_small(hip, mnk, offset):
+    m, n, k = mnk
+    a = oracle.to_f16_bits(oracle.uniform(700 + m, (m, k)))
+    b = oracle.to_f16_bits(oracle.uniform(701 + n, (k, n)))
+    ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b))
+    y = hip.gemm_f16(a, b, offset)
+    assert np.max(np.abs(y - ref)) <= 2e-3
+
+
+def test_gemm_pins(hip):
+    pins.pin_gemm(hip.gemm_f32)
+    f16 = lambda a, b: hip.gemm_f16(oracle.to_f16_bits(a), oracle.to_f16_bits(b))
+    pins.pin_gemm(f16)  # every pin input is exactly representable in fp16
+
+
+@pytest.mark.parametrize("dtype,size", [("f32", 4096), ("f32", 4095), ("f16", 4096),
+                                        ("f16", 4095), ("f16", 8192)])
+def test_gemm_baseline_sizes(hip, dtype, size):
+    a = oracle.uniform(800 + size, (size, size))
+    b = oracle.uniform(801 + size, (size, size))
+    rows = sample_rows(size, 14, 802)
+    if dtype == "f16":
+        a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(a, b)
+        ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b), rows)
+        assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b)
+        ref = oracle.gemm(a, b, rows)
+        assert np.linalg.norm(y[rows] - ref) / np.linalg.norm(ref) <= 1e-4
+    assert np.isfinite(y).all()
+
+
+# --------------------------------------------------------------------- attention
+
+# (S, D, causal, extreme): tests/attention_smoke.cu:168-173 plus edge shapes
+ATTN_SMALL = [(32, 64, False, False), (32, 128, True, False), (37, 71, True, True),
+              (1, 1, False, False), (5, 16, True, False), (129, 32, True, False),
+              (200, 96, False, False), (257, 128, True, False), (64, 40, False, False)]
+
+
+def _attn_inputs(s, d, extreme, seed, heads=2):
+    r = 20.0 if extreme else 1.0
+    q = oracle.uniform(seed, (1, heads, s, d), -r, r)
+    k = oracle.uniform(seed + 1, (1, heads, s, d), -r, r)
+    v = oracle.uniform(seed + 2, (1, heads, s, d))
+    return q, k, v
+
+
+@pytest.mark.parametrize("s,d,causal,extreme", ATTN_SMALL)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_attention_f32_small(hip, s, d, causal, extreme, offset):
+    q, k, v = _attn_inputs(s, d, extreme, 900 + s + d)
+    ref = oracle.attention(q, k, v, causal)
+    y = hip.attention(q, k, v, causal, offset)
+    assert np.all(np.abs(y - ref) <= 1e-4 + 1e-4 * np.abs(ref))
+
+
+@pytest.mark.parametrize("s,d,causal,extreme", ATTN_SMALL)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_attention_f16_small(hip, s, d, causal, extreme, offset):
+    q, k, v = _attn_inputs(s, d, extreme, 950 + s + d)
+    qb, kb, vb = (oracle.to_f16_bits(t) for t in (q, k, v))
+    ref = oracle.attention(*(oracle.from_f16_bits(t) for t in (qb, kb, vb)), causal)
+    y = hip.attention(qb, kb, vb, causal, offset)
+    # extreme (+-20) inputs use the reference's own 2e-2 bound
+    # (tests/attention_smoke.cu:154); the rest the BASELINE 2e-3
+    assert np.max(np.abs(y - ref)) <= (2e-2 if extreme else 2e-3)
+
+
+def test_attention_pins(hip):
+    pins.pin_attention(hip.attention, tol=2e-6)
+    f16 = lambda q, k, v, c: hip.attention(*(oracle.to_f16_bits(t) for t in (q, k, v)), c)
+    pins.pin_attention(f16, tol=1e-2)
+
+
+@pytest.mark.parametrize("b,h,s,causal,rows", [(1, 12, 1024, False, 768),
+                                               (1, 12, 1024, True, 768),
+                                               (4, 32, 8192, True, 160)])
+def test_attention_f16_baseline(hip, b, h, s, causal, rows):
+    d = 128
+    q, k, v = (oracle.to_f16_bits(oracle.normal(1000 + i, (b, h, s, d))) for i in range(3))
+    y = hip.attention(q, k, v, causal)
+    qf, kf, vf = (oracle.from_f16_bits(t) for t in (q, k, v))
+    rng = np.random.default_rng(1001)
+    heads = rng.integers(0, b * h, rows).astype(np.int32)
+    rws = rng.integers(0, s, rows).astype(np.int32)
+    # always include the first/last rows and the diagonal tile edges
+    extra_rows = np.array([0, 1, 127, 128, s - 1, s - 2], np.int32)
+    heads = np.concatenate([heads, np.zeros(6, np.int32), np.full(6, b * h - 1, np.int32)])
+    rws = np.concatenate([rws, extra_rows, extra_rows])
+    ref = oracle.attention(qf, kf, vf, causal, heads, rws)
+    got = y.reshape(b * h, s, d)[heads, rws]
+    assert np.max(np.abs(got - ref)) <= 2e-3
+    assert np.isfinite(y).all()
