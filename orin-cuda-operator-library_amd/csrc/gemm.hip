@@ -4,12 +4,15 @@
 //
 // Reference: operatorlib::gemm_f16 / gemm_f32 (src/gemm.cu:440-479). The
 // reference dispatches between WMMA, cp.async register-tiled and scalar
-// kernels on divisibility; here one MFMA kernel template serves every shape:
-// the "vector" instance stages 16-byte chunks and needs 16-byte aligned
-// rows, the "general" instance stages element by element with zero fill and
-// takes any shape and alignment (the 4095^3 edge case runs on MFMA too).
+// kernels on divisibility; here every path runs on MFMA:
+//   * gemm_f16_dma_kernel (fp16, K % 64 == 0, N % 8 == 0, 16-byte aligned
+//     operands): direct global->LDS loads, described before the kernel;
+//   * gemm_mfma_kernel "vector" instance: 16-byte register-staged chunks,
+//     16-byte aligned rows (all fp32 shapes with K, N % 4 == 0);
+//   * gemm_mfma_kernel "general" instance: element-wise staging with zero
+//     fill, any shape and alignment (the 4095^3 edge case runs on MFMA too).
 //
-// Tiling (both precisions):
+// Register-staged tiling (gemm_mfma_kernel, both precisions):
 //   * 256 x 256 C tile per 256-thread workgroup; 2 x 2 wavefronts, each
 //     owning a 128 x 128 sub-tile = 4 x 4 MFMA 32x32 blocks (256 fp32
 //     accumulators per lane, held in AGPR/VGPR at one wave per SIMD);
@@ -278,6 +281,219 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
   }
 }
 
+// ---------------------------------------------------------------------------
+// gemm_f16_dma_kernel — the fp16 fast path (K % 64 == 0, N % 8 == 0, 16-byte
+// aligned A and B).
+//
+//   * 256 x 256 C tile per 512-thread workgroup: 8 wavefronts as 2 (M) x 4
+//     (N), each owning 128 x 64 = 4 x 2 MFMA 32x32x16 blocks (128 fp32
+//     accumulators, so two wavefronts fit per SIMD and one's LDS waits are
+//     covered by the other's MFMAs);
+//   * A and B are copied global -> LDS by global_load_lds_dwordx4 (each lane
+//     writes 16 bytes at LDS base + 16 * lane), so operands never pass
+//     through VGPRs and no ds_write is issued;
+//   * both tiles keep their global layout (A [m][k], B [k][n]); B fragments
+//     are read with ds_read_b64_tr_b16, which returns k-contiguous fp16
+//     pairs from n-contiguous rows: within each 16-lane group, lane 4r + j
+//     addresses 4 elements of row r and lane i receives element i % 4 of
+//     the lanes 4r + i / 4, r = 0..3;
+//   * XOR swizzles of the 16-byte chunks make every read conflict-free:
+//     A rows (128 B) use chunk ^ ((m >> 1) & 7), B rows (512 B) chunk ^
+//     4 * (k & 3); the DMA lane -> chunk mapping applies the same swizzle,
+//     and it keeps 128-byte (A) / 512-byte (B) contiguous global segments;
+//   * two LDS stages in separate arrays (so the compiler can see that the
+//     DMA into one does not alias the reads of the other), the loop unrolled
+//     by two; fragments for step s+1 are read while step s runs on the
+//     matrix cores (sched_barrier keeps that order);
+//   * M / N edges: source rows / columns are clamped into the matrix (their
+//     results are never stored), stores are masked.
+// Measured on MI355X (8192^3): ~1.09 PFLOP/s, about 90% of hipBLASLt's
+// fp16 GEMM on the same box.
+// ---------------------------------------------------------------------------
+
+namespace dma {
+
+typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
+#define OPL_LDS __attribute__((address_space(3)))
+
+constexpr int kWM = 2, kWN = 4;
+constexpr int kThreads = 64 * kWM * kWN;  // 512
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kFM = kBM / kWM / 32;  // 4
+constexpr int kFN = kBN / kWN / 32;  // 2
+constexpr int kABytes = kBM * kBK * 2;  // 32 KiB, rows of 128 B
+constexpr int kBBytes = kBK * kBN * 2;  // 32 KiB, rows of 512 B
+constexpr int kStage = kABytes + kBBytes;
+constexpr int kCopies = kABytes / 16 / kThreads;  // DMA chunks per thread per operand (4)
+
+__device__ __forceinline__ int swizzle_a(int m) { return (m >> 1) & 7; }
+__device__ __forceinline__ int swizzle_b(int k) { return 4 * (k & 3); }
+
+struct Fragments {
+  half8 a[kFM];
+  half8 b[kFN];
+};
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
+                         const _Float16* __restrict__ B,
+                         float* __restrict__ C, int M, int N, int K) {
+  __shared__ __attribute__((aligned(1024))) unsigned char stage0[kStage];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage1[kStage];
+
+  const int tiles_m = (M + kBM - 1) / kBM;
+  const int tiles_n = (N + kBN - 1) / kBN;
+  int tm, tn;
+  tile_of_block(tiles_m, tiles_n, &tm, &tn);
+  const int m0 = tm * kBM;
+  const int n0 = tn * kBN;
+
+  const int lane = threadIdx.x % opl::kWaveSize;
+  const int wave = threadIdx.x / opl::kWaveSize;
+  const int wm = wave / kWN;
+  const int wn = wave % kWN;
+  const int half = lane / 32;
+  const int l32 = lane % 32;
+
+  // DMA sources: copy j of this thread fills LDS chunk slot
+  // (wave * kCopies + j) * 64 + lane of each operand tile.
+  const _Float16* a_src[kCopies];
+  const _Float16* b_src[kCopies];
+#pragma unroll
+  for (int j = 0; j < kCopies; ++j) {
+    const int slot = (wave * kCopies + j) * 64 + lane;
+    const int m = slot / 8;
+    const int chunk = (slot % 8) ^ swizzle_a(m);
+    a_src[j] = A + static_cast<std::size_t>(min(m0 + m, M - 1)) * K + 8 * chunk;
+    const int kk = (wave * kCopies + j) * 2 + lane / 32;
+    const int col = n0 + 8 * ((lane % 32) ^ swizzle_b(kk));
+    b_src[j] = B + static_cast<std::size_t>(kk) * N + min(col, N - 8);
+  }
+  auto issue = [&](unsigned char* stage, int k0) {
+    unsigned char* sb = stage + kABytes;
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j)
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void*>(a_src[j] + k0),
+          (OPL_LDS void*)(stage + (wave * kCopies + j) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j)
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void*>(b_src[j] + static_cast<std::size_t>(k0) * N),
+          (OPL_LDS void*)(sb + (wave * kCopies + j) * 1024), 16, 0, 0);
+  };
+
+  // Fragment byte offsets inside a stage for each of the 4 k16 steps.
+  int a_off[kFM][4];
+#pragma unroll
+  for (int ti = 0; ti < kFM; ++ti) {
+    const int m = wm * (kBM / kWM) + 32 * ti + l32;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      a_off[ti][s] = m * 128 + (((2 * s + half) ^ swizzle_a(m)) * 16);
+  }
+  const int group = lane / 16;
+  const int gl = lane % 16;
+  int b_off[kFN][4][2];
+#pragma unroll
+  for (int tj = 0; tj < kFN; ++tj)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int n = wn * (kBN / kWN) + 32 * tj + 16 * (group % 2) + 4 * (gl % 4);
+        const int k = 16 * s + 8 * (group / 2) + 4 * r + gl / 4;
+        b_off[tj][s][r] = kABytes + k * 512 +
+                          (((n / 8) ^ swizzle_b(k)) * 16) + (n % 8) * 2;
+      }
+
+  floatx16 acc[kFM][kFN];
+#pragma unroll
+  for (int i = 0; i < kFM; ++i)
+#pragma unroll
+    for (int j = 0; j < kFN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  auto load = [&](const unsigned char* st, int s, Fragments& f) {
+#pragma unroll
+    for (int ti = 0; ti < kFM; ++ti)
+      f.a[ti] = *reinterpret_cast<const half8*>(st + a_off[ti][s]);
+#pragma unroll
+    for (int tj = 0; tj < kFN; ++tj) {
+      const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+          (OPL_LDS fp16x4*)(st + b_off[tj][s][0]));
+      const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+          (OPL_LDS fp16x4*)(st + b_off[tj][s][1]));
+      half8 b;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        b[e] = lo[e];
+        b[4 + e] = hi[e];
+      }
+      f.b[tj] = b;
+    }
+  };
+  auto mma = [&](const Fragments& f) {
+#pragma unroll
+    for (int ti = 0; ti < kFM; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < kFN; ++tj)
+        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            f.a[ti], f.b[tj], acc[ti][tj], 0, 0, 0);
+  };
+
+  const int steps = K / kBK;
+  auto tile = [&](const unsigned char* cur, unsigned char* nxt, int step) {
+    if (step + 1 < steps) issue(nxt, (step + 1) * kBK);
+    __builtin_amdgcn_sched_barrier(0);
+    Fragments f0, f1;
+    load(cur, 0, f0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 4; s += 2) {
+      load(cur, s + 1, f1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 2 < 4) load(cur, s + 2, f0);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(f1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this step's reads and the next DMA
+    __syncthreads();
+  };
+
+  issue(stage0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int step = 0;
+  for (; step + 1 < steps; step += 2) {
+    tile(stage0, stage1, step);
+    tile(stage1, stage0, step + 1);
+  }
+  if (step < steps) tile(stage0, stage1, step);
+
+#pragma unroll
+  for (int ti = 0; ti < kFM; ++ti) {
+#pragma unroll
+    for (int tj = 0; tj < kFN; ++tj) {
+      const int col = n0 + wn * (kBN / kWN) + 32 * tj + l32;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row =
+            m0 + wm * (kBM / kWM) + 32 * ti + 8 * (e / 4) + 4 * half + (e % 4);
+        if (row < M && col < N)
+          C[static_cast<std::size_t>(row) * N + col] = acc[ti][tj][e];
+      }
+    }
+  }
+}
+
+#undef OPL_LDS
+}  // namespace dma
+
 template <typename T>
 hipError_t launch_gemm(const T* a, const T* b, float* c, int m, int n, int k,
                        hipStream_t stream) {
@@ -310,7 +526,18 @@ extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
                                     int m, int n, int k,
                                     void* stream_handle) {
   if (!opl::gemm_args_ok(a, b, c, m, n, k)) return hipErrorInvalidValue;
-  return launch_gemm<_Float16>(reinterpret_cast<const _Float16*>(a),
-                               reinterpret_cast<const _Float16*>(b), c, m, n,
-                               k, static_cast<hipStream_t>(stream_handle));
+  const _Float16* ha = reinterpret_cast<const _Float16*>(a);
+  const _Float16* hb = reinterpret_cast<const _Float16*>(b);
+  hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+  if (k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
+      opl::aligned16(b)) {
+    const long long tiles = static_cast<long long>((m + dma::kBM - 1) / dma::kBM) *
+                            ((n + dma::kBN - 1) / dma::kBN);
+    if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+    dma::gemm_f16_dma_kernel<<<dim3(static_cast<unsigned>(tiles)),
+                               dim3(dma::kThreads), 0, stream>>>(ha, hb, c, m,
+                                                                  n, k);
+    return hipGetLastError();
+  }
+  return launch_gemm<_Float16>(ha, hb, c, m, n, k, stream);
 }

@@ -10,7 +10,7 @@ namespace {
 
 struct ScratchRegistry {
   std::mutex mutex;
-  std::map<std::pair<int, hipStream_t>, ReduceScratch> by_stream;
+  std::map<std::pair<int, hipStream_t>, double*> by_stream;
 };
 
 ScratchRegistry& registry() {
@@ -22,7 +22,7 @@ ScratchRegistry& registry() {
 
 }  // namespace
 
-hipError_t reduce_scratch_for_stream(hipStream_t stream, ReduceScratch* out) {
+hipError_t reduce_partials_for_stream(hipStream_t stream, double** out) {
   int device = 0;
   hipError_t status = hipGetDevice(&device);
   if (status != hipSuccess) return status;
@@ -34,26 +34,11 @@ hipError_t reduce_scratch_for_stream(hipStream_t stream, ReduceScratch* out) {
     *out = found->second;
     return hipSuccess;
   }
-  // Layout: [counter (256 B slot)] [partials: kReduceMaxBlocks doubles].
-  constexpr std::size_t kCounterSlot = 256;
-  const std::size_t bytes =
-      kCounterSlot + sizeof(double) * static_cast<std::size_t>(kReduceMaxBlocks);
   void* base = nullptr;
-  status = hipMalloc(&base, bytes);
+  status = hipMalloc(&base, sizeof(double) * kReduceMaxBlocks);
   if (status != hipSuccess) return status;
-  // Zero the counter on the consumer's stream, so it is ordered before the
-  // first reduce that uses it without any device-wide synchronization.
-  status = hipMemsetAsync(base, 0, kCounterSlot, stream);
-  if (status != hipSuccess) {
-    (void)hipFree(base);
-    return status;
-  }
-  ReduceScratch scratch;
-  scratch.counter = static_cast<unsigned*>(base);
-  scratch.partials = reinterpret_cast<double*>(static_cast<char*>(base) +
-                                               kCounterSlot);
-  reg.by_stream.emplace(key, scratch);
-  *out = scratch;
+  reg.by_stream.emplace(key, static_cast<double*>(base));
+  *out = static_cast<double*>(base);
   return hipSuccess;
 }
 

@@ -167,9 +167,13 @@ def test_rmsnorm_pins(hip):
 
 # -------------------------------------------------------------------------- gemm
 
+# The reference smoke matrix (tests/gemm_smoke.cu:141-148) plus shapes that
+# exercise this library's fp16 global->LDS path at its M / N edges (K % 64 == 0,
+# N % 8 == 0, partial 256-wide tiles) and its fallback paths.
 GEMM_SMALL = [(1, 256, 64), (16, 128, 64), (128, 64, 32), (37, 65, 71), (7, 37, 23),
               (128, 128, 32), (16, 128, 32), (32, 32, 32), (17, 19, 23),
-              (256, 256, 256), (300, 520, 200), (513, 129, 1000)]
+              (256, 256, 256), (300, 520, 200), (513, 129, 1000),
+              (300, 520, 192), (513, 136, 1024), (1, 8, 64), (1000, 1000, 128)]
 
 
 @pytest.mark.parametrize("mnk", GEMM_SMALL)
