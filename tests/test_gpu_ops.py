@@ -226,10 +226,13 @@ def test_gemm_baseline_sizes(hip, dtype, size):
 
 # --------------------------------------------------------------------- attention
 
-# (S, D, causal, extreme): tests/attention_smoke.cu:168-173 plus edge shapes
+# (S, D, causal, extreme): tests/attention_smoke.cu:168-173, edge shapes, and
+# shapes on this library's fp16 global->LDS path (D 64/128, S % 128 == 0).
 ATTN_SMALL = [(32, 64, False, False), (32, 128, True, False), (37, 71, True, True),
               (1, 1, False, False), (5, 16, True, False), (129, 32, True, False),
-              (200, 96, False, False), (257, 128, True, False), (64, 40, False, False)]
+              (200, 96, False, False), (257, 128, True, False), (64, 40, False, False),
+              (128, 128, True, False), (256, 64, True, False), (384, 64, False, False),
+              (512, 128, False, True)]
 
 
 def _attn_inputs(s, d, extreme, seed, heads=2):
