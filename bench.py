@@ -39,7 +39,7 @@ sys.path.insert(0, str(REPO))
 sys.path.insert(0, str(REPO / "orin-cuda-operator-library_amd"))
 
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
-FP16_PEAK_TFLOPS = 2500.0       # dense FP16 MFMA (BASELINE roofline uses 2516.6)
+FP16_PEAK_TFLOPS = 2500.0       # dense FP16 MFMA (AMD lists 2516.6)
 FP32_PEAK_TFLOPS = 157.3        # FP32 matrix
 ROTATE_BYTES = 512 * 2 ** 20    # > MALL (256 MB): cold-cache rotation target
 
@@ -70,7 +70,7 @@ PROFILE_OPS = {"copy", "reduce", "softmax", "rmsnorm", "transpose", "gemm_f32", 
 
 
 def profile_only(torch, lib, oracle, ptr, op: str, launches: int) -> None:
-    """A few launches of one kernel at its BASELINE size, nothing timed."""
+    """A few launches of one kernel at its benchmark size, nothing timed."""
     dev = "cuda"
     stream = torch.cuda.current_stream().cuda_stream
     gen = torch.Generator(device=dev).manual_seed(1)
@@ -210,6 +210,18 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         return e
 
     want = (lambda n: True) if names == "all" else (lambda n: n in names.split(","))
+
+    if want("copy"):
+        # Not an operatorlib op: a plain 64 MiB device-to-device copy, the
+        # practical streaming ceiling the bandwidth kernels are read against.
+        n = 16 * 2 ** 20
+        sets = sets_for(8 * n)
+        xs = [(torch.rand(n, device=dev), torch.empty(n, device=dev)) for _ in range(sets)]
+        f = lambda i: xs[i % sets][1].copy_(xs[i % sets][0])
+        e = bw_entry("device_copy (torch, ceiling reference)", [n], 8 * n,
+                     *time_single(torch, f, steps, warmup))
+        out.append(e)
+        del xs
 
     if want("reduce"):
         n = 16_777_216
@@ -352,7 +364,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
-              "(each operator is a single-GPU kernel; see DESIGN.md for how it would shard).",
+              "(each operator is a single-GPU kernel; sharding is not built).",
               file=sys.stderr)
         sys.exit(2)
 

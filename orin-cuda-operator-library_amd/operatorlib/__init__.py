@@ -56,9 +56,9 @@ _clib = None
 _torch_loaded = False
 
 
-def build(verbose: bool = False, torch_binding: bool = True, smoke: bool = True) -> None:
+def build(verbose: bool = False, torch_binding: bool = True) -> None:
     """Compile every native artefact for gfx950 (see ``_build``)."""
-    _build.build(verbose=verbose, torch_binding=torch_binding, smoke=smoke)
+    _build.build(verbose=verbose, torch_binding=torch_binding)
 
 
 def _require(path: Path) -> None:

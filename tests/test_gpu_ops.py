@@ -1,6 +1,6 @@
 """GPU parity tests: HIP kernels (through the C ABI) against the CPU oracle.
 
-Tolerances are the BASELINE contract, written here:
+Tolerances (the benchmark contract in BASELINE.json), written here:
   transpose                bit-exact
   reduce                   |y - ref| <= 1e-5 |ref|           (ref fp64)
   softmax, rmsnorm         elementwise max |y-ref|/|ref| over |ref| >= 1e-30,
@@ -11,7 +11,7 @@ Tolerances are the BASELINE contract, written here:
   attention_f32            |y - ref| <= 1e-4 + 1e-4 |ref| (the reference's
                            tests/attention_smoke.cu:108 bound)
 Small shapes hit every dispatch path of the reference (its smoke-test shape
-matrix) and of this library; BASELINE shapes run at full size, checked in
+matrix) and of this library; benchmark shapes run at full size, checked in
 full where the oracle is fast and on seeded row samples (always including
 the first and last rows) where it is not.
 """
@@ -260,7 +260,7 @@ def test_attention_f16_small(hip, s, d, causal, extreme, offset):
     ref = oracle.attention(*(oracle.from_f16_bits(t) for t in (qb, kb, vb)), causal)
     y = hip.attention(qb, kb, vb, causal, offset)
     # extreme (+-20) inputs use the reference's own 2e-2 bound
-    # (tests/attention_smoke.cu:154); the rest the BASELINE 2e-3
+    # (tests/attention_smoke.cu:154); the rest the 2e-3 contract
     assert np.max(np.abs(y - ref)) <= (2e-2 if extreme else 2e-3)
 
 

@@ -1,0 +1,170 @@
+"""CPU-side checks of the library boundary (no GPU needed, no kernel runs).
+
+* liboperatorlib.so loads and exports every function include/*.h declares;
+* the C and C++ headers compile on their own (C99 for the C ABI);
+* argument validation rejects the reference's invalid inputs with
+  hipErrorInvalidValue before any HIP call (src/reduce.cu:56-57,
+  src/softmax.cu:184-185, src/transpose.cu:40-41, src/rmsnorm.cu:80-82,
+  src/attention.cu:448-451, :489-492), so it is testable without a device;
+* the torch extension registers the reference's schema strings byte for
+  byte (python/operatorlib_binding.cpp:190-197);
+* the C++ API keeps the reference's function names and order
+  (include/operatorlib/operators.h:13-44).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import operatorlib
+
+REPO = Path(__file__).resolve().parents[1]
+INCLUDE = REPO / "include"
+C_HEADER = INCLUDE / "operatorlib" / "operatorlib_c.h"
+CPP_HEADER = INCLUDE / "operatorlib" / "operators.h"
+
+REFERENCE_SCHEMA = [
+    "reduce_sum(Tensor input) -> Tensor",
+    "softmax(Tensor input) -> Tensor",
+    "transpose(Tensor input) -> Tensor",
+    "rmsnorm(Tensor input, Tensor weight, float epsilon=1e-5) -> Tensor",
+    "gemm(Tensor a, Tensor b) -> Tensor",
+    "attention(Tensor q, Tensor k, Tensor v, bool causal=False) -> Tensor",
+]
+BINDING_SOURCE = REPO / "orin-cuda-operator-library_amd" / "csrc" / "torch_binding.cpp"
+
+REFERENCE_API = ["reduce_sum_f32", "softmax_f32", "transpose_f32", "rmsnorm_f32",
+                 "gemm_f32", "gemm_f16", "attention_f32", "attention_f16"]
+
+INVALID = operatorlib.HIP_ERROR_INVALID_VALUE
+FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails validation
+NULL = None
+
+
+def declared_c_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", C_HEADER.read_text(), flags=re.S)
+    return re.findall(r"\b(operatorlib_\w+)\s*\(", text)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return operatorlib.clib()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_c_functions()
+    assert len(names) == 10, names
+    assert set(names) == set(operatorlib.C_SYMBOLS)
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_exported_dynamic_symbols_are_exactly_the_abi():
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", str(operatorlib.LIBRARY_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines()
+                if ln.split() and ln.split()[-1].startswith("operatorlib_")}
+    assert exported == set(declared_c_functions())
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.operatorlib_abi_version() == 1
+    assert lib.operatorlib_status_string(0)
+    assert b"invalid" in lib.operatorlib_status_string(INVALID).lower()
+
+
+def test_c_header_is_plain_c99(tmp_path):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = tmp_path / "abi.c"
+    src.write_text("#include <operatorlib/operatorlib_c.h>\n"
+                   "int main(void) { return operatorlib_abi_version() == "
+                   "OPERATORLIB_ABI_VERSION ? 0 : 1; }\n")
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-pedantic", "-I", str(INCLUDE),
+                    "-c", str(src), "-o", str(tmp_path / "abi.o")], check=True)
+
+
+def test_cpp_api_names_and_order():
+    text = CPP_HEADER.read_text()
+    names = re.findall(r"inline\s+hipError_t\s+(\w+)\s*\(", text)
+    assert names == REFERENCE_API
+    assert text.count("hipStream_t stream = nullptr") == len(REFERENCE_API)
+
+
+# -------------------------------------------------- validation before any HIP call
+
+def test_reduce_rejects(lib):
+    assert lib.operatorlib_reduce_sum_f32(NULL, FAKE, 10, NULL) == INVALID
+    assert lib.operatorlib_reduce_sum_f32(FAKE, NULL, 10, NULL) == INVALID
+    assert lib.operatorlib_reduce_sum_f32(FAKE, FAKE, 0, NULL) == INVALID
+
+
+@pytest.mark.parametrize("fn", ["operatorlib_softmax_f32", "operatorlib_transpose_f32"])
+@pytest.mark.parametrize("args", [(NULL, FAKE, 4, 4), (FAKE, NULL, 4, 4), (FAKE, FAKE, 0, 4),
+                                  (FAKE, FAKE, 4, 0), (FAKE, FAKE, -1, 4), (FAKE, FAKE, 4, -7)])
+def test_matrix_ops_reject(lib, fn, args):
+    assert getattr(lib, fn)(*args, NULL) == INVALID
+
+
+@pytest.mark.parametrize("args", [
+    (NULL, FAKE, FAKE, 2, 8, 1e-5), (FAKE, NULL, FAKE, 2, 8, 1e-5), (FAKE, FAKE, NULL, 2, 8, 1e-5),
+    (FAKE, FAKE, FAKE, 0, 8, 1e-5), (FAKE, FAKE, FAKE, 2, 0, 1e-5),
+    (FAKE, FAKE, FAKE, 2, 8, 0.0), (FAKE, FAKE, FAKE, 2, 8, -1e-5),
+    (FAKE, FAKE, FAKE, 2, 8, float("nan"))])
+def test_rmsnorm_rejects(lib, args):
+    assert lib.operatorlib_rmsnorm_f32(*args, NULL) == INVALID
+
+
+@pytest.mark.parametrize("fn", ["operatorlib_gemm_f32", "operatorlib_gemm_f16"])
+@pytest.mark.parametrize("args", [(NULL, FAKE, FAKE, 4, 4, 4), (FAKE, NULL, FAKE, 4, 4, 4),
+                                  (FAKE, FAKE, NULL, 4, 4, 4), (FAKE, FAKE, FAKE, 0, 4, 4),
+                                  (FAKE, FAKE, FAKE, 4, 0, 4), (FAKE, FAKE, FAKE, 4, 4, 0)])
+def test_gemm_rejects(lib, fn, args):
+    assert getattr(lib, fn)(*args, NULL) == INVALID
+
+
+@pytest.mark.parametrize("fn", ["operatorlib_attention_f32", "operatorlib_attention_f16"])
+@pytest.mark.parametrize("args", [
+    (NULL, FAKE, FAKE, FAKE, 1, 1, 8, 16), (FAKE, NULL, FAKE, FAKE, 1, 1, 8, 16),
+    (FAKE, FAKE, NULL, FAKE, 1, 1, 8, 16), (FAKE, FAKE, FAKE, NULL, 1, 1, 8, 16),
+    (FAKE, FAKE, FAKE, FAKE, 0, 1, 8, 16), (FAKE, FAKE, FAKE, FAKE, 1, 0, 8, 16),
+    (FAKE, FAKE, FAKE, FAKE, 1, 1, 0, 16), (FAKE, FAKE, FAKE, FAKE, 1, 1, 8, 0),
+    (FAKE, FAKE, FAKE, FAKE, 1, 1, 8, 129),
+    (FAKE, FAKE, FAKE, FAKE, 65536, 65536, 8, 16)])   # batch * heads > INT32_MAX
+def test_attention_rejects(lib, fn, args):
+    assert getattr(lib, fn)(*args, 0, NULL) == INVALID
+
+
+# ------------------------------------------------------------- torch schema
+
+def test_torch_schema_source_is_byte_identical():
+    defs = re.findall(r'm\.def\("([^"]*)"\)', BINDING_SOURCE.read_text())
+    assert defs == REFERENCE_SCHEMA
+
+
+def test_torch_schema_matches_reference():
+    import torch
+    operatorlib.load_operatorlib()
+    for text in REFERENCE_SCHEMA:
+        name = text.split("(")[0]
+        got = getattr(torch.ops.operatorlib, name).default._schema
+        assert got == torch._C.parse_schema("operatorlib::" + text), (got, text)
+
+
+def test_torch_ops_have_no_cpu_kernel():
+    """Registered on the CUDA key only, as the reference binding is
+    (python/operatorlib_binding.cpp:199-206): no silent CPU path."""
+    import torch
+    operatorlib.load_operatorlib()
+    with pytest.raises(NotImplementedError):
+        torch.ops.operatorlib.softmax(torch.ones(2, 2))
