@@ -41,6 +41,7 @@
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "common.hpp"
 #include "operatorlib/operatorlib_c.h"
@@ -450,6 +451,9 @@ typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
 #define OPL_LDS __attribute__((address_space(3)))
 
 constexpr int kKeys = 64;
+constexpr int kXcds = 8;
+// Headroom (log2 units) the running row max may lag the true max by.
+constexpr float kLazyLog2 = 8.0f;
 
 template <int D>
 struct Layout {
@@ -479,9 +483,20 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   __shared__ __attribute__((aligned(1024))) unsigned char stage0[L::kStage];
   __shared__ __attribute__((aligned(1024))) unsigned char stage1[L::kStage];
 
+  // Work item w = (head, query block) in head-major order, heaviest query
+  // block first within a head. Workgroups are dealt to the 8 XCDs
+  // round-robin; XCD x takes the contiguous range of work items
+  // [x * per_xcd, (x + 1) * per_xcd), so the workgroups resident on one XCD
+  // at a time belong to one or two heads and share that head's K/V tiles
+  // in the XCD's L2 instead of streaming them from HBM per query block.
   const int q_blocks = S / kBlockRows;
-  const int qb = q_blocks - 1 - static_cast<int>(blockIdx.x / BH);
-  const int bh = static_cast<int>(blockIdx.x % BH);
+  const int total = q_blocks * BH;
+  const int per_xcd = (total + kXcds - 1) / kXcds;
+  const int w = static_cast<int>(blockIdx.x % kXcds) * per_xcd +
+                static_cast<int>(blockIdx.x / kXcds);
+  if (w >= total) return;  // padding of the grid to a multiple of 8
+  const int bh = w / q_blocks;
+  const int qb = q_blocks - 1 - w % q_blocks;
   const int q0 = qb * kBlockRows;
   const int lane = threadIdx.x % opl::kWaveSize;
   const int wave = threadIdx.x / opl::kWaveSize;
@@ -558,59 +573,69 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     if (t + 1 < tiles) issue(nxt, key0 + kKeys);
     __builtin_amdgcn_sched_barrier(0);
     if (!causal || key0 <= wave_row0 + kRowsPerWave - 1) {
-      floatx16 s[2];
+      // The tile is processed as two 32-key halves. Lazy rescaling (below)
+      // lets half 1 be exponentiated against the running max before its
+      // own max is checked (it is recomputed in the rare case the max must
+      // move), so one basic block holds the scores of half 1, the P.V
+      // product of half 0 (matrix cores) and the exponentials of both
+      // halves (vector ALUs), and the scheduler can interleave them.
+      auto scores = [&](int kb) {
+        floatx16 s;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
+        for (int e = 0; e < 16; ++e) s[e] = 0.0f;
 #pragma unroll
         for (int c = 0; c < L::kSteps; ++c) {
           const half8 a = *reinterpret_cast<const half8*>(
               cur + k_off[c] + kb * 32 * L::kRowBytes);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s[kb], 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
         }
-      }
-      const bool needs_mask = causal && key0 + kKeys - 1 > wave_row0;
-      float tile_max = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        return s;
+      };
+      auto mask = [&](floatx16& s, int kb) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          float x = s[kb][e] * score_scale_log2;
-          if (needs_mask) {
-            const int key = key0 + 32 * kb + 8 * (e / 4) + 4 * half + (e % 4);
-            if (key > my_row) x = -INFINITY;
-          }
-          s[kb][e] = x;
-          tile_max = fmaxf(tile_max, x);
+          const int key = key0 + 32 * kb + 8 * (e / 4) + 4 * half + (e % 4);
+          if (key > my_row) s[e] = -INFINITY;
         }
-      tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-      const float new_max = fmaxf(row_max, tile_max);
-      const float alpha = opl::fast_exp2(row_max - new_max);
-      row_max = new_max;
-      float psum = 0.0f;
+      };
+      // Row max of a half (log2 units), both lane halves combined.
+      auto scaled_max = [&](const floatx16& s) {
+        float m = s[0];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = opl::fast_exp2(s[kb][e] - new_max);
-          s[kb][e] = p;
-          psum += p;
-        }
-      row_sum = row_sum * alpha + psum;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+        for (int e = 1; e < 16; ++e) m = fmaxf(m, s[e]);
+        return fmaxf(m, __shfl_xor(m, 32)) * score_scale_log2;
+      };
+      // Lazy rescaling: the running max m (log2 units) only moves when a
+      // row's max exceeds it by more than kLazyLog2, so p = 2^(x - m) stays
+      // <= 2^kLazyLog2 (well inside fp16's range) and the O rescale is
+      // skipped on almost every half-tile. Softmax is shift-invariant: the
+      // result is the same up to rounding.
+      auto needs_move = [&](float cand) {
+        return __builtin_amdgcn_ballot_w64(cand > row_max + kLazyLog2) != 0;
+      };
+      auto move_max = [&](float cand) {
+        const float new_max = fmaxf(row_max, cand);
+        const float alpha = opl::fast_exp2(row_max - new_max);
+        row_max = new_max;
+        row_sum *= alpha;
 #pragma unroll
         for (int dt = 0; dt < L::kDTiles; ++dt)
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-      }
+      };
+      auto exponentiate = [&](const floatx16& s, half8 (&pb)[2]) {
+        float psum = 0.0f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int e = 0; e < 16; ++e) {
+          const float p = opl::fast_exp2(fmaf(s[e], score_scale_log2, -row_max));
+          psum += p;
+          pb[e / 8][e % 8] = static_cast<_Float16>(p);
+        }
+        return psum;
+      };
+      auto accumulate = [&](int kb, const half8 (&pb)[2]) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          half8 pb;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(s[kb][8 * u + e]);
           const int rows = (32 * kb + 16 * u) * L::kRowBytes;
 #pragma unroll
           for (int dt = 0; dt < L::kDTiles; ++dt) {
@@ -624,9 +649,35 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
               a[e] = lo[e];
               a[4 + e] = hi[e];
             }
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[u], o[dt], 0, 0, 0);
           }
         }
+      };
+      auto body = [&](auto masked_tag) {
+        constexpr bool kMasked = decltype(masked_tag)::value;
+        half8 p0[2], p1[2];
+        floatx16 s0 = scores(0);
+        if constexpr (kMasked) mask(s0, 0);
+        const float c0 = scaled_max(s0);
+        if (needs_move(c0)) move_max(c0);
+        floatx16 s1 = scores(1);
+        row_sum += exponentiate(s0, p0);
+        accumulate(0, p0);
+        if constexpr (kMasked) mask(s1, 1);
+        const float c1 = scaled_max(s1);
+        float ps1 = exponentiate(s1, p1);
+        if (needs_move(c1)) {
+          move_max(c1);  // after P.V of half 0, which used the old max
+          ps1 = exponentiate(s1, p1);
+        }
+        row_sum += ps1;
+        accumulate(1, p1);
+      };
+      // Only tiles crossing the diagonal are masked (a wave-uniform test).
+      if (causal && key0 + kKeys - 1 > wave_row0)
+        body(std::true_type{});
+      else
+        body(std::false_type{});
     }
     __builtin_amdgcn_s_waitcnt(0);  // this tile's reads and the next DMA
     __syncthreads();
@@ -675,7 +726,7 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
   const int bh = batch * heads;
   const long long blocks =
       static_cast<long long>((sequence + kBlockRows - 1) / kBlockRows) * bh;
-  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (blocks > 0x7fffffffLL - 8) return hipErrorInvalidValue;
   constexpr int E = 16 / sizeof(T);
   const bool vector_ok = head_dim % E == 0 && opl::aligned16(q) &&
                          opl::aligned16(k) && opl::aligned16(v) &&
@@ -686,7 +737,9 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
     if (f16_dma_ok(q, k, v, out, sequence, head_dim)) {
       const float scale =
           1.4426950408889634f / sqrtf(static_cast<float>(head_dim));
-      const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+      // a multiple of 8 workgroups, one contiguous range of work per XCD
+      const long long padded = (blocks + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
+      const dim3 grid(static_cast<unsigned>(padded)), block(kThreads);
       if (head_dim == 128)
         dma::attention_f16_dma_kernel<128><<<grid, block, 0, stream>>>(
             q, k, v, out, bh, sequence, c, scale);

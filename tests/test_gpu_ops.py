@@ -232,7 +232,7 @@ ATTN_SMALL = [(32, 64, False, False), (32, 128, True, False), (37, 71, True, Tru
               (1, 1, False, False), (5, 16, True, False), (129, 32, True, False),
               (200, 96, False, False), (257, 128, True, False), (64, 40, False, False),
               (128, 128, True, False), (256, 64, True, False), (384, 64, False, False),
-              (512, 128, False, True)]
+              (512, 128, False, True), (256, 128, True, True)]
 
 
 def _attn_inputs(s, d, extreme, seed, heads=2):
@@ -262,6 +262,19 @@ def test_attention_f16_small(hip, s, d, causal, extreme, offset):
     # extreme (+-20) inputs use the reference's own 2e-2 bound
     # (tests/attention_smoke.cu:154); the rest the 2e-3 contract
     assert np.max(np.abs(y - ref)) <= (2e-2 if extreme else 2e-3)
+
+
+@pytest.mark.parametrize("heads,s,d,causal", [(1, 384, 128, True), (3, 384, 64, True),
+                                               (9, 256, 128, False), (5, 128, 64, True)])
+def test_attention_f16_fast_path_covers_every_block(hip, heads, s, d, causal):
+    # (heads x query blocks) not a multiple of 8: the work items are split
+    # over 8 XCD ranges and the grid is padded; every row must be written.
+    q, k, v = _attn_inputs(s, d, False, 970 + heads + s, heads=heads)
+    qb, kb, vb = (oracle.to_f16_bits(t) for t in (q, k, v))
+    ref = oracle.attention(*(oracle.from_f16_bits(t) for t in (qb, kb, vb)), causal)
+    y = hip.attention(qb, kb, vb, causal)
+    assert np.isfinite(y).all()
+    assert np.max(np.abs(y - ref)) <= 2e-3
 
 
 def test_attention_pins(hip):
