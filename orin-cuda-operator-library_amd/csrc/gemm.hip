@@ -41,6 +41,7 @@
 
 #include "common.hpp"
 #include "operatorlib/operatorlib_c.h"
+#include "scratch.hpp"
 #include "validate.hpp"
 
 namespace {
@@ -130,7 +131,7 @@ struct Stager {
   }
 
   // Global -> registers for the K step starting at k0.
-  __device__ __forceinline__ void load(const T* A, const T* B, int M, int N,
+  __device__ __forceinline__ void load(const T* A, const T* B, int M, int ldb,
                                        int K, int m0, int n0, int k0) {
     const int tid = threadIdx.x;
 #pragma unroll
@@ -147,7 +148,7 @@ struct Stager {
       const int j = q / (kBK / E);  // n-chunk
 #pragma unroll
       for (int r = 0; r < E; ++r)
-        b[blk][r] = load_chunk(B, N, k0 + g * E + r, K, n0 + j * E, N);
+        b[blk][r] = load_chunk(B, ldb, k0 + g * E + r, K, n0 + j * E, ldb);
     }
   }
 
@@ -199,7 +200,7 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n,
 template <typename T, bool kVector>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
-                      float* __restrict__ C, int M, int N, int K) {
+                      float* __restrict__ C, int M, int N, int K, int ldb) {
   using P = Precision<T>;
   using Chunk = typename P::Chunk;
   using S = Stager<T, kVector>;
@@ -229,7 +230,7 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 
   const int steps = (K + S::kBK - 1) / S::kBK;
   S stager;
-  stager.load(A, B, M, N, K, m0, n0, 0);
+  stager.load(A, B, M, ldb, K, m0, n0, 0);
   stager.store(lds);
   __syncthreads();
 
@@ -245,7 +246,7 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
   for (int step = 0; step < steps; ++step) {
     const unsigned char* stage = lds + (step & 1) * kStageBytes;
     if (step + 1 < steps)
-      stager.load(A, B, M, N, K, m0, n0, (step + 1) * S::kBK);
+      stager.load(A, B, M, ldb, K, m0, n0, (step + 1) * S::kBK);
 #pragma unroll
     for (int p = 0; p < kChunksPerRow / 2; ++p) {
       const int chunk = (2 * p + half) * 16;
@@ -337,7 +338,7 @@ struct Fragments {
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
                          const _Float16* __restrict__ B,
-                         float* __restrict__ C, int M, int N, int K) {
+                         float* __restrict__ C, int M, int N, int K, int ldb) {
   __shared__ __attribute__((aligned(1024))) unsigned char stage0[kStage];
   __shared__ __attribute__((aligned(1024))) unsigned char stage1[kStage];
 
@@ -367,7 +368,7 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
     a_src[j] = A + static_cast<std::size_t>(min(m0 + m, M - 1)) * K + 8 * chunk;
     const int kk = (wave * kCopies + j) * 2 + lane / 32;
     const int col = n0 + 8 * ((lane % 32) ^ swizzle_b(kk));
-    b_src[j] = B + static_cast<std::size_t>(kk) * N + min(col, N - 8);
+    b_src[j] = B + static_cast<std::size_t>(kk) * ldb + min(col, ldb - 8);
   }
   auto issue = [&](unsigned char* stage, int k0) {
     unsigned char* sb = stage + kABytes;
@@ -379,7 +380,7 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
 #pragma unroll
     for (int j = 0; j < kCopies; ++j)
       __builtin_amdgcn_global_load_lds(
-          static_cast<const void*>(b_src[j] + static_cast<std::size_t>(k0) * N),
+          static_cast<const void*>(b_src[j] + static_cast<std::size_t>(k0) * ldb),
           (OPL_LDS void*)(sb + (wave * kCopies + j) * 1024), 16, 0, 0);
   };
 
@@ -494,20 +495,118 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
 #undef OPL_LDS
 }  // namespace dma
 
+// Copies a row-major [rows, cols] matrix into a zero-padded row-major
+// [rows_p, cols_p] one (cols_p a multiple of one 16-byte chunk, 16-byte
+// aligned destination): each thread writes whole chunks.
+template <typename T>
+__global__ __launch_bounds__(256) void pad_copy_kernel(
+    const T* __restrict__ src, int rows, int cols, T* __restrict__ dst,
+    int rows_p, int cols_p) {
+  using Chunk = typename Precision<T>::Chunk;
+  constexpr int E = Precision<T>::kChunkElems;
+  const long long per_row = cols_p / E;
+  const long long total = static_cast<long long>(rows_p) * per_row;
+  for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+       i < total; i += static_cast<long long>(gridDim.x) * blockDim.x) {
+    const int r = static_cast<int>(i / per_row);
+    const int c0 = static_cast<int>(i % per_row) * E;
+    const T* s = src + static_cast<std::size_t>(r) * cols;
+    Chunk v;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      v[e] = (r < rows && c0 + e < cols) ? s[c0 + e] : T(0);
+    *reinterpret_cast<Chunk*>(dst + static_cast<std::size_t>(r) * cols_p + c0) = v;
+  }
+}
+
+template <typename T>
+void launch_pad_copy(const T* src, int rows, int cols, T* dst, int rows_p,
+                     int cols_p, hipStream_t stream) {
+  constexpr int E = Precision<T>::kChunkElems;
+  const long long chunks = static_cast<long long>(rows_p) * (cols_p / E);
+  const long long blocks = (chunks + 255) / 256;
+  pad_copy_kernel<T><<<dim3(static_cast<unsigned>(blocks < 8192 ? blocks : 8192)),
+                       dim3(256), 0, stream>>>(src, rows, cols, dst, rows_p,
+                                               cols_p);
+}
+
+inline long long round_up(long long x, long long to) { return (x + to - 1) / to * to; }
+
+// Large GEMMs whose operands miss the fast kernels' rules (K or N not a
+// multiple of the chunk / K step, or unaligned pointers; the 4095^3 edge
+// case) are run on zero-padded aligned copies: the copies cost a few
+// percent of the product at these sizes, the element-wise general kernel
+// several times more. Zero rows/columns of K contribute nothing; padded
+// columns of N are never stored.
+inline bool worth_padding(int m, int n, int k) {
+  return m >= 128 && n >= 128 && 2.0 * m * n * static_cast<double>(k) >= 1073741824.0;
+}
+
+struct PaddedOperands {
+  const void* a;
+  const void* b;
+  int k;    // padded K (row stride of A)
+  int ldb;  // row stride of B
+};
+
+// Pads A to [m, kp] and/or B to [kp, np] in the stream's workspace as needed.
+template <typename T>
+hipError_t pad_operands(const T* a, const T* b, int m, int n, int k, int k_mult,
+                        int n_mult, hipStream_t stream, PaddedOperands* out) {
+  const long long kp = round_up(k, k_mult);
+  const long long np = round_up(n, n_mult);
+  const bool pad_a = kp != k || !opl::aligned16(a);
+  const bool pad_b = kp != k || np != n || !opl::aligned16(b);
+  if (kp > 0x7fffffffLL || np > 0x7fffffffLL) return hipErrorInvalidValue;
+  const std::size_t a_bytes =
+      pad_a ? static_cast<std::size_t>(round_up(static_cast<long long>(m) * kp * sizeof(T), 256)) : 0;
+  const std::size_t b_bytes = pad_b ? static_cast<std::size_t>(kp * np * sizeof(T)) : 0;
+  void* ws = nullptr;
+  hipError_t status = opl::workspace_for_stream(stream, a_bytes + b_bytes, &ws);
+  if (status != hipSuccess) return status;
+  T* pa = static_cast<T*>(ws);
+  T* pb = reinterpret_cast<T*>(static_cast<unsigned char*>(ws) + a_bytes);
+  if (pad_a) launch_pad_copy<T>(a, m, k, pa, m, static_cast<int>(kp), stream);
+  if (pad_b)
+    launch_pad_copy<T>(b, k, n, pb, static_cast<int>(kp), static_cast<int>(np), stream);
+  out->a = pad_a ? static_cast<const void*>(pa) : a;
+  out->b = pad_b ? static_cast<const void*>(pb) : b;
+  out->k = static_cast<int>(kp);
+  out->ldb = pad_b ? static_cast<int>(np) : n;
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_gemm(const T* a, const T* b, float* c, int m, int n, int k,
                        hipStream_t stream) {
   constexpr int E = Precision<T>::kChunkElems;
-  const bool vector_ok = k % E == 0 && n % E == 0 && opl::aligned16(a) &&
-                         opl::aligned16(b);
   const long long tiles = static_cast<long long>((m + kBM - 1) / kBM) *
                           ((n + kBN - 1) / kBN);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
-  if (vector_ok)
-    gemm_mfma_kernel<T, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k);
-  else
-    gemm_mfma_kernel<T, false><<<grid, block, 0, stream>>>(a, b, c, m, n, k);
+  const bool vector_ok = k % E == 0 && n % E == 0 && opl::aligned16(a) &&
+                         opl::aligned16(b);
+  if (vector_ok) {
+    gemm_mfma_kernel<T, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k, n);
+  } else if (worth_padding(m, n, k)) {
+    PaddedOperands p;
+    const hipError_t status = pad_operands<T>(a, b, m, n, k, E, E, stream, &p);
+    if (status != hipSuccess) return status;
+    gemm_mfma_kernel<T, true><<<grid, block, 0, stream>>>(
+        static_cast<const T*>(p.a), static_cast<const T*>(p.b), c, m, n, p.k, p.ldb);
+  } else {
+    gemm_mfma_kernel<T, false><<<grid, block, 0, stream>>>(a, b, c, m, n, k, n);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_f16_dma(const _Float16* a, const _Float16* b, float* c,
+                               int m, int n, int k, int ldb, hipStream_t stream) {
+  const long long tiles = static_cast<long long>((m + dma::kBM - 1) / dma::kBM) *
+                          ((n + dma::kBN - 1) / dma::kBN);
+  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+  dma::gemm_f16_dma_kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(dma::kThreads),
+                             0, stream>>>(a, b, c, m, n, k, ldb);
   return hipGetLastError();
 }
 
@@ -530,14 +629,16 @@ extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
   const _Float16* hb = reinterpret_cast<const _Float16*>(b);
   hipStream_t stream = static_cast<hipStream_t>(stream_handle);
   if (k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
-      opl::aligned16(b)) {
-    const long long tiles = static_cast<long long>((m + dma::kBM - 1) / dma::kBM) *
-                            ((n + dma::kBN - 1) / dma::kBN);
-    if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-    dma::gemm_f16_dma_kernel<<<dim3(static_cast<unsigned>(tiles)),
-                               dim3(dma::kThreads), 0, stream>>>(ha, hb, c, m,
-                                                                  n, k);
-    return hipGetLastError();
+      opl::aligned16(b))
+    return launch_gemm_f16_dma(ha, hb, c, m, n, k, n, stream);
+  if (worth_padding(m, n, k)) {
+    PaddedOperands p;
+    const hipError_t status =
+        pad_operands<_Float16>(ha, hb, m, n, k, dma::kBK, 8, stream, &p);
+    if (status != hipSuccess) return status;
+    return launch_gemm_f16_dma(static_cast<const _Float16*>(p.a),
+                               static_cast<const _Float16*>(p.b), c, m, n, p.k,
+                               p.ldb, stream);
   }
   return launch_gemm<_Float16>(ha, hb, c, m, n, k, stream);
 }

@@ -200,6 +200,45 @@ def test_gemm_f16_small(hip, mnk, offset):
     assert np.max(np.abs(y - ref)) <= 2e-3
 
 
+# Large shapes that miss the fast kernels' rules and run on zero-padded
+# copies of A and/or B (K or N off the chunk multiple, or unaligned).
+GEMM_PADDED = [(1000, 1000, 1000), (1024, 1030, 1024), (1100, 1000, 999), (640, 768, 1800)]
+
+
+@pytest.mark.parametrize("mnk", GEMM_PADDED)
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_gemm_padded_operands(hip, mnk, offset, dtype):
+    m, n, k = mnk
+    a = oracle.uniform(620 + m, (m, k))
+    b = oracle.uniform(621 + n, (k, n))
+    rows = np.unique(np.concatenate([np.arange(40), np.arange(m - 40, m),
+                                     np.random.default_rng(m + n).integers(0, m, 48)]))
+    if dtype == "f16":
+        ab, bb = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(ab, bb, offset)
+        ref = oracle.gemm(oracle.from_f16_bits(ab), oracle.from_f16_bits(bb), rows)
+        assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b, offset)
+        ref = oracle.gemm(a, b, rows)
+        assert np.linalg.norm(y[rows] - ref) / np.linalg.norm(ref) <= 1e-4
+    assert np.isfinite(y).all()
+
+
+def test_gemm_padded_then_smaller(hip):
+    """The per-stream workspace is reused: a large padded call followed by a
+    smaller one (and a larger one, which grows it) must all be right."""
+    for m, n, k in [(1200, 1100, 1001), (700, 800, 1999), (1500, 1500, 1500)]:
+        a = oracle.uniform(630 + m, (m, k))
+        b = oracle.uniform(631 + n, (k, n))
+        ab, bb = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(ab, bb)
+        rows = np.array([0, 1, m // 2, m - 2, m - 1])
+        ref = oracle.gemm(oracle.from_f16_bits(ab), oracle.from_f16_bits(bb), rows)
+        assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+
+
 def test_gemm_pins(hip):
     pins.pin_gemm(hip.gemm_f32)
     f16 = lambda a, b: hip.gemm_f16(oracle.to_f16_bits(a), oracle.to_f16_bits(b))
