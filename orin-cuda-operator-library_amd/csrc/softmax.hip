@@ -63,7 +63,7 @@ __global__ __launch_bounds__(opl::kRowWaveThreads) void softmax_wave_kernel(
   const int row = blockIdx.x * opl::kRowWaveRows + threadIdx.x / opl::kWaveSize;
   if (row >= rows) return;  // uniform per wavefront
   const std::size_t offset = static_cast<std::size_t>(row) * cols;
-  opl::RowSlice<V, opl::kWaveSize, W> s;
+  typename opl::SliceFor<V, opl::kWaveSize, W>::type s;
   s.load(input + offset, cols, lane, -INFINITY);
   const float m = opl::wave_reduce<opl::MaxOp>(local_max(s.x));
   const float sum = opl::wave_reduce<opl::SumOp>(exp_shift_sum(s.x, m));
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(opl::kRowBlockThreads) void softmax_block_kernel(
   __shared__ float max_slots[opl::kRowBlockWaves];
   __shared__ float sum_slots[opl::kRowBlockWaves];
   const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
-  opl::RowSlice<V, opl::kRowBlockThreads, W> s;
+  typename opl::SliceFor<V, opl::kRowBlockThreads, W>::type s;
   s.load(input + offset, cols, threadIdx.x, -INFINITY);
   const float m = opl::block_reduce<opl::MaxOp, opl::kRowBlockWaves>(
       local_max(s.x), max_slots);
@@ -162,8 +162,8 @@ void launch_block(int v, const float* in, float* out, int rows, int cols,
   if constexpr (V < MaxV) {
     if (v > V) return launch_block<W, 2 * V, MaxV>(v, in, out, rows, cols, stream);
   }
-  softmax_block_kernel<V, W><<<dim3(rows), dim3(opl::kRowBlockThreads), 0,
-                               stream>>>(in, out, cols);
+  softmax_block_kernel<V, W><<<dim3(rows), dim3(opl::kRowBlockThreads),
+                               0, stream>>>(in, out, cols);
 }
 
 }  // namespace
@@ -176,14 +176,20 @@ extern "C" int operatorlib_softmax_f32(const float* input, float* output,
   hipStream_t stream = static_cast<hipStream_t>(stream_handle);
   const bool vec4 =
       cols % 4 == 0 && opl::aligned16(input) && opl::aligned16(output);
-  const opl::RowPlan plan = opl::pick_row_plan(cols, vec4);
+  // Ragged rows (cols % 4 != 0 or unaligned) keep 16-byte accesses when
+  // input and output rows share their 16-byte phase.
+  const bool ragged = !vec4 && opl::same_phase16(input, output) &&
+                      cols >= opl::kRaggedMinCols;
+  const opl::RowPlan plan = opl::pick_row_plan(cols, vec4 || ragged);
   switch (plan.path) {
     case opl::RowPath::kWave:
       if (vec4) launch_wave<4, 1, 16>(plan.per_thread, input, output, rows, cols, stream);
+      else if (ragged) launch_wave<0, 1, 16>(plan.per_thread, input, output, rows, cols, stream);
       else launch_wave<1, 1, 64>(plan.per_thread, input, output, rows, cols, stream);
       break;
     case opl::RowPath::kBlock:
       if (vec4) launch_block<4, 4, 16>(plan.per_thread, input, output, rows, cols, stream);
+      else if (ragged) launch_block<0, 4, 16>(plan.per_thread, input, output, rows, cols, stream);
       else launch_block<1, 16, 64>(plan.per_thread, input, output, rows, cols, stream);
       break;
     case opl::RowPath::kTwoPass:

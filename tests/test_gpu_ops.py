@@ -94,7 +94,7 @@ SOFTMAX_SHAPES = [(19, 128), (17, 1024), (17, 1003), (5, 1), (3, 7), (1, 4096),
 
 
 @pytest.mark.parametrize("shape", SOFTMAX_SHAPES)
-@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("offset", [0, 1, 2, 3])
 def test_softmax_matches_oracle(hip, shape, offset):
     x = oracle.normal(200 + shape[1], shape, 0.0, 3.0)
     ref = oracle.softmax(x)
@@ -116,6 +116,49 @@ def test_softmax_extreme_scale(hip, shape):
 
 def test_softmax_pins(hip):
     pins.pin_softmax(hip.softmax, tol=2e-7)
+
+
+# Input and output in different 16-byte phases (rows cannot share one
+# float4 layout): the element-wise paths. The weight of RMSNorm may sit at
+# any alignment on every path.
+MIXED_SHAPES = [(17, 1003), (5, 1), (3, 7), (3, 9000), (4097, 1023), (2, 40000)]
+
+
+def _rows_call(lib, name, x, in_off, out_off, weight=None, eps=0.0):
+    """softmax / rmsnorm through the C ABI with independent input and output
+    offsets (elements into their allocations)."""
+    from gpu_util import check, empty, ptr, stream_handle, to_device
+    d = to_device(x, in_off)
+    out = empty(x.shape, out_off)
+    rows, cols = x.shape
+    fn = getattr(lib, name)
+    if weight is None:
+        check(fn(ptr(d), ptr(out), rows, cols, stream_handle()), name)
+    else:
+        check(fn(ptr(d), ptr(weight), ptr(out), rows, cols, eps, stream_handle()), name)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("shape", MIXED_SHAPES)
+@pytest.mark.parametrize("in_off,out_off", [(1, 0), (0, 3), (2, 1)])
+def test_softmax_mixed_phases(lib, shape, in_off, out_off):
+    x = oracle.normal(260 + shape[1], shape, 0.0, 3.0)
+    y = _rows_call(lib, "operatorlib_softmax_f32", x, in_off, out_off)
+    elem, norm = rel_errors(y, oracle.softmax(x))
+    assert elem <= 1e-5 and norm <= 1e-5, (elem, norm)
+
+
+@pytest.mark.parametrize("shape", MIXED_SHAPES)
+@pytest.mark.parametrize("in_off,out_off,w_off", [(1, 0, 0), (0, 3, 1), (2, 2, 1), (3, 3, 0)])
+def test_rmsnorm_mixed_phases(lib, shape, in_off, out_off, w_off):
+    from gpu_util import to_device
+    x = oracle.normal(560 + shape[1], shape)
+    w = oracle.uniform(561, shape[1], 0.5, 1.5)
+    y = _rows_call(lib, "operatorlib_rmsnorm_f32", x, in_off, out_off,
+                   to_device(w, w_off), 1e-5)
+    elem, norm = rel_errors(y, oracle.rmsnorm(x, w, 1e-5))
+    assert elem <= 1e-5 and norm <= 1e-5, (elem, norm)
 
 
 # --------------------------------------------------------------------- transpose
@@ -151,7 +194,7 @@ RMSNORM_CASES = [((32, 4096), 1e-5), ((17, 1003), 1e-5), ((21, 1024), 1e-5),
 
 
 @pytest.mark.parametrize("shape,eps", RMSNORM_CASES)
-@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("offset", [0, 1, 2, 3])
 def test_rmsnorm_matches_oracle(hip, shape, eps, offset):
     x = oracle.normal(500 + shape[1], shape)
     w = oracle.uniform(501, shape[1], 0.5, 1.5)
