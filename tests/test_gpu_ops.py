@@ -164,7 +164,9 @@ def test_rmsnorm_mixed_phases(lib, shape, in_off, out_off, w_off):
 # --------------------------------------------------------------------- transpose
 
 TRANSPOSE_SHAPES = [(37, 65), (64, 96), (65, 37), (1, 1), (1, 1000), (1000, 1),
-                    (64, 64), (129, 257), (4096, 4096), (4095, 4097)]
+                    (64, 64), (129, 257), (4096, 4096), (4095, 4097),
+                    # rows, cols % 4 == 0: the float4 kernel, partial 128-tiles
+                    (4, 8), (132, 260), (520, 128), (128, 516), (4, 4096), (1024, 4)]
 
 
 @pytest.mark.parametrize("shape", TRANSPOSE_SHAPES)
