@@ -11,9 +11,11 @@ the measured step time. Inputs are resident in HBM before timing; steps
 rotate through 6 buffer sets (~604 MB > the 256 MB MALL) so each step
 streams from HBM, not from cache.
 
-Timing: torch.cuda.synchronize(), a short untimed spin kernel (so the host
-queues every launch before the GPU reaches them), then K steps bracketed by
-one pair of HIP events recorded on the launch stream, then synchronize.
+Timing: W untimed warm-up steps (and at least 0.15 s of them, so timing
+starts at the clocks the GPU holds under the load, not during its ramp),
+torch.cuda.synchronize(), a short untimed spin kernel (so the host queues
+every launch before the GPU reaches them), then K steps bracketed by one
+pair of HIP events recorded on the launch stream, then synchronize.
 Per-kernel durations (roofline, ops) come from separate regions of
 back-to-back launches of that kernel, timed the same way.
 
@@ -177,10 +179,26 @@ def time_region(torch, launch, launches):
     return start.elapsed_time(end) / launches
 
 
-def time_single(torch, launch, steps, warmup):
-    """(mean ms per launch, mean ms per launch) after `warmup` untimed launches."""
-    for i in range(warmup):
+WARM_SECONDS = 0.15  # untimed launches before each timed region
+
+
+def warm_up(torch, launch, min_launches):
+    """Untimed launches: at least `min_launches` and at least WARM_SECONDS of
+    wall time, so the timed region starts at the clocks the GPU settles at
+    under this load rather than during its ramp."""
+    i, t0 = 0, time.perf_counter()
+    while i < min_launches or time.perf_counter() - t0 < WARM_SECONDS:
         launch(i)
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return i
+
+
+def time_single(torch, launch, steps, warmup):
+    """(mean ms per launch, mean ms per launch) after the warm-up."""
+    warm_up(torch, launch, warmup)
     ms = time_region(torch, launch, steps)
     return ms, ms
 
@@ -383,10 +401,12 @@ def main():
         return
 
     work = Rowwise(torch, lib, oracle, ptr)
-    for i in range(args.warmup):
+
+    def step(i):
         work.softmax(i)
         work.rmsnorm(i)
-    torch.cuda.synchronize()
+
+    warm_up(torch, step, args.warmup)
 
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     spin(torch)
