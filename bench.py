@@ -312,6 +312,30 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
                             *time_single(torch, f, reps, 3), peak, extra))
         del da, db, c
 
+    # Decode-shaped GEMMs (the reference's M == 1 and M <= 16 configurations):
+    # HBM-bound on B, reported in GB/s of algorithmic traffic (A, B, C once).
+    for name, m in (("gemm_f32", 1), ("gemm_f32", 16), ("gemm_f16", 1), ("gemm_f16", 16)):
+        if not want("gemm_skinny") and not want("gemm"):
+            break
+        n = k = 4096
+        es = 2 if name == "gemm_f16" else 4
+        gen = torch.Generator(device=dev).manual_seed(27)
+        sets = sets_for(k * n * es)
+        bs = [(torch.rand((k, n), device=dev, generator=gen) * 2 - 1) for _ in range(sets)]
+        a = torch.rand((m, k), device=dev, generator=gen) * 2 - 1
+        if es == 2:
+            bs = [x.half() for x in bs]
+            a = a.half()
+        c = torch.empty((m, n), device=dev)
+        fn = lib.operatorlib_gemm_f16 if es == 2 else lib.operatorlib_gemm_f32
+        f = lambda i: fn(ptr(a), ptr(bs[i % sets]), ptr(c), m, n, k, stream)
+        ms_med, ms_mean = time_single(torch, f, steps, warmup)
+        nbytes = (m * k + k * n) * es + m * n * 4
+        e = bw_entry(f"{name} skinny", [m, n, k], nbytes, ms_med, ms_mean)
+        e["TFLOPs"] = round(2 * m * n * k / (ms_med * 1e-3) / 1e12, 3)
+        out.append(e)
+        del bs, a, c
+
     attn_cases = [(1, 12, 1024, False), (1, 12, 1024, True), (4, 32, 8192, True)]
     for bsz, heads, seq, causal in attn_cases:
         if not want("attention"):

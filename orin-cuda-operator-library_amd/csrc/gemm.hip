@@ -38,6 +38,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "common.hpp"
 #include "operatorlib/operatorlib_c.h"
@@ -495,6 +496,287 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
 #undef OPL_LDS
 }  // namespace dma
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM, M <= 16 (the reference's M == 1 and M <= 16 configurations,
+// src/gemm.cu:445-448 and :464-467; LLM decode shapes such as 1 x 4096 x
+// 4096). The product is a stream over B (K x N): 2 MNK flops for 2-4 bytes
+// of B per (k, n) pair, far below the matrix cores' balance, so the kernel
+// is built to stream B at HBM rate with vector-ALU dot products:
+//   * a 256-thread workgroup takes a 256-byte-wide column block of B (64
+//     fp32 or 128 fp16 columns) and a chunk of K rows; 16 lanes cover one
+//     row segment with 16-byte loads, 16 rows are in flight per step;
+//   * the workgroup's A chunk is staged in LDS transposed ([k][m]), so a
+//     lane reads the M values for its row with 16-byte LDS reads that all
+//     16 lanes of the row share;
+//   * fp16 multiplies pairs of rows with v_dot2_f32_f16 (two products per
+//     instruction, fp32 accumulation), fp32 uses FMAs;
+//   * partial sums reduce across the 4 lanes per wavefront that share a
+//     column (lane shuffles), then across the 4 wavefronts through LDS, in
+//     a fixed order;
+//   * K is split over enough workgroups to fill the GPU; per-split partials
+//     go to the stream's workspace and a second kernel sums them in split
+//     order, so results are deterministic.
+namespace skinny {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kMaxM = 16;
+constexpr int kLanesPerRow = 16;                     // one 256-byte row segment
+constexpr int kRowGroups = kThreads / kLanesPerRow;  // 16
+constexpr int kWaves = kThreads / opl::kWaveSize;    // 4
+constexpr int kMaxChunk = 512;                       // K rows per workgroup
+
+template <typename T>
+struct Cfg {
+  static constexpr int kPerLane = 16 / sizeof(T);       // columns per lane
+  static constexpr int kBlockN = kLanesPerRow * kPerLane;  // 64 fp32, 128 fp16
+  static constexpr int kRowsPerStep = sizeof(T) == 2 ? 2 : 1;  // dot2 pairs
+};
+
+// Row steps (16-byte loads of one or two rows) in flight per thread per
+// batch, sized so accumulators (M x 4 or M x 8 floats) plus the batch stay
+// within 256 VGPRs, i.e. at least two wavefronts per SIMD.
+template <typename T, int M>
+constexpr int batch_for() {
+  return sizeof(T) == 2 ? (M <= 2 ? 8 : (M <= 4 ? 4 : 2)) : (M <= 4 ? 8 : 4);
+}
+
+// One 16-byte chunk of B (P columns of row r) and, for fp16, of row r + 1;
+// rows at or past k_end read a valid row and are zeroed.
+template <typename T>
+struct RowChunk {
+  using Vec = typename std::conditional<sizeof(T) == 2, half8, float4v>::type;
+  Vec v[Cfg<T>::kRowsPerStep];
+};
+
+template <typename T>
+__device__ __forceinline__ RowChunk<T> load_rows(const T* __restrict__ B, int n,
+                                                 int col, int r, int k_end) {
+  RowChunk<T> c;
+#pragma unroll
+  for (int s = 0; s < Cfg<T>::kRowsPerStep; ++s) {
+    const int row = r + s;
+    const int rc = row < k_end ? row : k_end - 1;
+    using Vec = typename RowChunk<T>::Vec;
+    Vec v = *reinterpret_cast<const Vec*>(B + static_cast<std::size_t>(rc) * n + col);
+    if (row >= k_end) {
+#pragma unroll
+      for (int j = 0; j < Cfg<T>::kPerLane; ++j) v[j] = T(0);
+    }
+    c.v[s] = v;
+  }
+  return c;
+}
+
+template <typename T, int M>
+__device__ __forceinline__ void accumulate_rows(const RowChunk<T>& c,
+                                                const float* ak,
+                                                float (&acc)[M][Cfg<T>::kPerLane]) {
+  constexpr int P = Cfg<T>::kPerLane;
+  if constexpr (sizeof(T) == 2) {
+    half2v bp[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      bp[j][0] = c.v[0][j];
+      bp[j][1] = c.v[1][j];
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const half2v a = __builtin_bit_cast(half2v, ak[m]);
+#pragma unroll
+      for (int j = 0; j < P; ++j)
+        acc[m][j] = __builtin_amdgcn_fdot2(a, bp[j], acc[m][j], false);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float a = ak[m];
+#pragma unroll
+      for (int j = 0; j < P; ++j) acc[m][j] = fmaf(a, c.v[0][j], acc[m][j]);
+    }
+  }
+}
+
+template <typename T, int M>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void skinny_kernel(
+    const T* __restrict__ A, const T* __restrict__ B, float* __restrict__ out,
+    int m_rows, int n, int k, int chunk) {
+  using C = Cfg<T>;
+  constexpr int P = C::kPerLane;
+  constexpr int R = C::kRowsPerStep;
+  // A chunk, transposed: fp32 as [k][M]; fp16 as [k / 2][M] pairs (k, k+1).
+  // One extra all-zero row (index kMaxChunk / R) absorbs batch steps past
+  // the chunk.
+  constexpr int kStage = (kMaxChunk / R + 1) * M;
+  constexpr int kStagePerThread = (kStage + kThreads - 1) / kThreads;
+  __shared__ __attribute__((aligned(16))) float a_lds[kStage];
+  __shared__ float red[kWaves * M * C::kBlockN];
+
+  constexpr int kBatch = batch_for<T, M>();
+  const int n0 = blockIdx.x * C::kBlockN;
+  const int k0 = blockIdx.y * chunk;
+  const int k_end = min(k, k0 + chunk);
+  const int steps = (k_end - k0 + R - 1) / R;  // rows (fp16: row pairs)
+  const int tid = threadIdx.x;
+  const int lane_col = tid % kLanesPerRow;
+  const int group = tid / kLanesPerRow;
+  // Columns past N: read a valid chunk (n % P == 0), results not stored.
+  const int col = min(n0 + lane_col * P, n - P);
+
+  // A values of this chunk (zeros past k_end and past m_rows) into
+  // registers first, then the first batch of B rows, then A into LDS: the
+  // B loads' latency overlaps the staging and its barrier.
+  float a_reg[kStagePerThread];
+#pragma unroll
+  for (int s = 0; s < kStagePerThread; ++s) {
+    const int i = tid + kThreads * s;
+    const int kk = i / M;
+    const int m = i % M;
+    float v = 0.0f;
+    if (i < chunk / R * M && m < m_rows) {
+      if constexpr (R == 2) {
+        half2v h;
+        const int r = k0 + 2 * kk;
+        h[0] = r < k_end ? A[static_cast<std::size_t>(m) * k + r] : T(0);
+        h[1] = r + 1 < k_end ? A[static_cast<std::size_t>(m) * k + r + 1] : T(0);
+        v = __builtin_bit_cast(float, h);
+      } else {
+        const int r = k0 + kk;
+        v = r < k_end ? static_cast<float>(A[static_cast<std::size_t>(m) * k + r]) : 0.0f;
+      }
+    }
+    a_reg[s] = v;
+  }
+  RowChunk<T> b[kBatch];
+#pragma unroll
+  for (int u = 0; u < kBatch; ++u)
+    b[u] = load_rows<T>(B, n, col, k0 + R * (group + kRowGroups * u), k_end);
+#pragma unroll
+  for (int s = 0; s < kStagePerThread; ++s) {
+    const int i = tid + kThreads * s;
+    if (i < kStage) a_lds[i] = a_reg[s];
+  }
+  __syncthreads();
+
+  float acc[M][P];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < P; ++j) acc[m][j] = 0.0f;
+
+  for (int base = group;; base += kBatch * kRowGroups) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      // Steps past `steps` read zeroed B rows and zero A slots (staged as
+      // zero past k_end, or the zero row past the chunk).
+      const int kk = min(base + kRowGroups * u, kMaxChunk / R);
+      accumulate_rows<T, M>(b[u], a_lds + kk * M, acc);
+    }
+    const int next = base + kBatch * kRowGroups;
+    if (next >= steps) break;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      b[u] = load_rows<T>(B, n, col, k0 + R * (next + kRowGroups * u), k_end);
+  }
+
+  // Lanes l, l^16, l^32, l^48 of a wavefront share a column chunk.
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      float v = acc[m][j];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[m][j] = v;
+    }
+  const int wave = tid / opl::kWaveSize;
+  const int lane = tid % opl::kWaveSize;
+  if (lane < kLanesPerRow) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int j = 0; j < P; ++j)
+        red[(wave * M + m) * C::kBlockN + lane * P + j] = acc[m][j];
+  }
+  __syncthreads();
+  float* dst = out + static_cast<std::size_t>(blockIdx.y) * m_rows * n;
+  for (int i = tid; i < M * C::kBlockN; i += kThreads) {
+    const int m = i / C::kBlockN;
+    const int c = i % C::kBlockN;
+    if (m < m_rows && n0 + c < n) {
+      float s = red[m * C::kBlockN + c];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) s += red[(w * M + m) * C::kBlockN + c];
+      dst[static_cast<std::size_t>(m) * n + n0 + c] = s;
+    }
+  }
+}
+
+// out[i] = sum over splits s (in order) of part[s][i].
+__global__ __launch_bounds__(256) void sum_splits_kernel(
+    const float* __restrict__ part, float* __restrict__ out, long long count,
+    int splits) {
+  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < count;
+       i += static_cast<long long>(gridDim.x) * 256) {
+    float s = part[i];
+    for (int p = 1; p < splits; ++p) s += part[p * count + i];
+    out[i] = s;
+  }
+}
+
+template <typename T, int M>
+void launch_m(const T* a, const T* b, float* dst, int m, int n, int k,
+              int chunk, dim3 grid, hipStream_t stream) {
+  skinny_kernel<T, M><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k, chunk);
+}
+
+template <typename T>
+bool applies(const T* b, int m, int n) {
+  return m <= kMaxM && n % Cfg<T>::kPerLane == 0 && opl::aligned16(b);
+}
+
+template <typename T>
+hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k,
+                  hipStream_t stream) {
+  using C = Cfg<T>;
+  const int blocks_n = (n + C::kBlockN - 1) / C::kBlockN;
+  // Enough workgroups to cover the GPU about twice; chunks of at most
+  // kMaxChunk rows, a multiple of 32.
+  int splits = (512 + blocks_n - 1) / blocks_n;
+  const int max_splits = (k + 63) / 64;
+  if (splits > max_splits) splits = max_splits;
+  if (splits < 1) splits = 1;
+  int chunk = (k + splits - 1) / splits;
+  chunk = (chunk + 31) / 32 * 32;
+  if (chunk > kMaxChunk) chunk = kMaxChunk;
+  splits = (k + chunk - 1) / chunk;
+  float* dst = c;
+  if (splits > 1) {
+    void* ws = nullptr;
+    const hipError_t status = opl::workspace_for_stream(
+        stream, static_cast<std::size_t>(splits) * m * n * sizeof(float), &ws);
+    if (status != hipSuccess) return status;
+    dst = static_cast<float*>(ws);
+  }
+  const dim3 grid(static_cast<unsigned>(blocks_n), static_cast<unsigned>(splits));
+  if (m == 1) launch_m<T, 1>(a, b, dst, m, n, k, chunk, grid, stream);
+  else if (m <= 2) launch_m<T, 2>(a, b, dst, m, n, k, chunk, grid, stream);
+  else if (m <= 4) launch_m<T, 4>(a, b, dst, m, n, k, chunk, grid, stream);
+  else if (m <= 8) launch_m<T, 8>(a, b, dst, m, n, k, chunk, grid, stream);
+  else launch_m<T, 16>(a, b, dst, m, n, k, chunk, grid, stream);
+  if (splits > 1) {
+    const long long count = static_cast<long long>(m) * n;
+    const long long blocks = (count + 255) / 256;
+    sum_splits_kernel<<<dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
+                        dim3(256), 0, stream>>>(dst, c, count, splits);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace skinny
+
 // Copies a row-major [rows, cols] matrix into a zero-padded row-major
 // [rows_p, cols_p] one (cols_p a multiple of one 16-byte chunk, 16-byte
 // aligned destination): each thread writes whole chunks.
@@ -616,8 +898,9 @@ extern "C" int operatorlib_gemm_f32(const float* a, const float* b, float* c,
                                     int m, int n, int k,
                                     void* stream_handle) {
   if (!opl::gemm_args_ok(a, b, c, m, n, k)) return hipErrorInvalidValue;
-  return launch_gemm<float>(a, b, c, m, n, k,
-                            static_cast<hipStream_t>(stream_handle));
+  hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+  if (skinny::applies(b, m, n)) return skinny::launch<float>(a, b, c, m, n, k, stream);
+  return launch_gemm<float>(a, b, c, m, n, k, stream);
 }
 
 extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
@@ -628,6 +911,7 @@ extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
   const _Float16* ha = reinterpret_cast<const _Float16*>(a);
   const _Float16* hb = reinterpret_cast<const _Float16*>(b);
   hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+  if (skinny::applies(hb, m, n)) return skinny::launch<_Float16>(ha, hb, c, m, n, k, stream);
   if (k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
       opl::aligned16(b))
     return launch_gemm_f16_dma(ha, hb, c, m, n, k, n, stream);

@@ -245,6 +245,38 @@ def test_gemm_f16_small(hip, mnk, offset):
     assert np.max(np.abs(y - ref)) <= 2e-3
 
 
+# M <= 16 (decode shapes): the skinny kernels, with and without K splits,
+# partial column blocks and odd K.
+GEMM_SKINNY = [(1, 4096, 4096), (4, 4096, 4096), (16, 4096, 4096), (3, 1000, 333),
+               (16, 4104, 1000), (1, 8, 5000), (9, 136, 777), (2, 64, 31), (1, 1024, 1)]
+
+
+@pytest.mark.parametrize("mnk", GEMM_SKINNY)
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_gemm_skinny(hip, mnk, dtype):
+    m, n, k = mnk
+    a = oracle.uniform(640 + m, (m, k))
+    b = oracle.uniform(641 + n, (k, n))
+    if dtype == "f16":
+        ab, bb = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(ab, bb)
+        ref = oracle.gemm(oracle.from_f16_bits(ab), oracle.from_f16_bits(bb))
+        assert np.max(np.abs(y - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b)
+        ref = oracle.gemm(a, b)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
+        assert np.all(np.abs(y - ref) <= 1e-3 + 1e-3 * np.abs(ref))
+
+
+def test_gemm_skinny_deterministic(hip):
+    a = oracle.uniform(650, (8, 4096))
+    b = oracle.uniform(651, (4096, 2048))
+    first = hip.gemm_f32(a, b)
+    for _ in range(3):
+        assert np.array_equal(hip.gemm_f32(a, b), first)
+
+
 # Large shapes that miss the fast kernels' rules and run on zero-padded
 # copies of A and/or B (K or N off the chunk multiple, or unaligned).
 GEMM_PADDED = [(1000, 1000, 1000), (1024, 1030, 1024), (1100, 1000, 999), (640, 768, 1800)]
