@@ -3,6 +3,7 @@
 Outputs (all under ``orin-cuda-operator-library_amd/operatorlib/lib``):
   * ``liboperatorlib.so``      — HIP kernels + the C ABI
                                  (include/operatorlib/operatorlib_c.h)
+  * ``operatorlib_run``        — standalone key=value runner (runner/)
   * ``_operatorlib_torch.so``  — ``torch.ops.operatorlib.*`` registrations
                                  (same schema as the reference's
                                  python/operatorlib_binding.cpp:190-206)
@@ -111,10 +112,24 @@ def build_torch_binding(verbose: bool = False) -> Path:
     return TORCH_EXT
 
 
+RUNNER = LIB_DIR / "operatorlib_run"
+
+
+def build_runner(verbose: bool = False) -> Path:
+    """The standalone key=value runner (runner/operatorlib_run.cpp)."""
+    src = PKG_ROOT / "runner" / "operatorlib_run.cpp"
+    tmp = RUNNER.with_name(RUNNER.name + ".tmp")
+    _run([HIPCC, *COMMON_FLAGS, str(src), f"-L{LIB_DIR}", "-loperatorlib",
+          "-Wl,-rpath,$ORIGIN", "-o", str(tmp)], verbose)
+    os.replace(tmp, RUNNER)
+    return RUNNER
+
+
 def build(verbose: bool = False, torch_binding: bool = True) -> None:
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     build_library(verbose)
+    build_runner(verbose)
     if torch_binding:
         build_torch_binding(verbose)
 
