@@ -452,6 +452,23 @@ typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKeys = 64;
 constexpr int kXcds = 8;
+// Word 3 of a raw (untyped, unswizzled) buffer resource on gfx9-family
+// parts: 32-bit data format, no index stride; only the byte range matters.
+constexpr int kBufferFlags = 0x00020000;
+
+// 16 bytes per lane from base + voffset + soffset into LDS at dst + 16 *
+// lane (dst wave-uniform), through a buffer resource over [base, base +
+// bytes): the base lives in scalar registers, offsets past `bytes` read
+// zeros. Kept out of the kernel bodies so the host pass never sees the
+// device-only resource type.
+__device__ __forceinline__ void buffer_copy16_lds(const void* base, unsigned bytes,
+                                                  unsigned char* dst, int voffset,
+                                                  int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                        bytes, kBufferFlags),
+      (OPL_LDS void*)dst, 16, voffset, soffset, 0, 0);
+}
 // Headroom (log2 units) the running row max may lag the true max by.
 constexpr float kLazyLog2 = 8.0f;
 
@@ -499,6 +516,8 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   const int qb = q_blocks - 1 - w % q_blocks;
   const int q0 = qb * kBlockRows;
   const int lane = threadIdx.x % opl::kWaveSize;
+  // (Kept as a vector value: declaring it wave-uniform turns the causal
+  // tests into scalar branches and measured ~8% slower.)
   const int wave = threadIdx.x / opl::kWaveSize;
   const int half = lane / 32;
   const int l32 = lane % 32;
@@ -525,20 +544,26 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     k_src[j] = row * D + 8 * (phys ^ L::swizzle_k(row));
     v_src[j] = row * D + 8 * (phys ^ L::swizzle_v(row));
   }
+  // Buffer resources over this head's K and V (the launcher guarantees
+  // S * D * 2 < 2^32): the per-lane byte offsets stay in 32-bit VGPRs and
+  // the tile's position is a scalar offset, so a tile's copies cost no
+  // vector address arithmetic.
+  const unsigned head_bytes = static_cast<unsigned>(S) * D * 2u;
+#pragma unroll
+  for (int j = 0; j < L::kCopies; ++j) {
+    k_src[j] *= 2;  // elements -> bytes
+    v_src[j] *= 2;
+  }
   auto issue = [&](unsigned char* st, int key0) {
-    const _Float16* kt = kh + static_cast<std::size_t>(key0) * D;
-    const _Float16* vt = vh + static_cast<std::size_t>(key0) * D;
+    const int tile_bytes = key0 * D * 2;
 #pragma unroll
     for (int j = 0; j < L::kCopies; ++j)
-      __builtin_amdgcn_global_load_lds(
-          static_cast<const void*>(kt + k_src[j]),
-          (OPL_LDS void*)(st + (wave * L::kCopies + j) * 1024), 16, 0, 0);
+      buffer_copy16_lds(kh, head_bytes, st + (wave * L::kCopies + j) * 1024,
+                        k_src[j], tile_bytes);
 #pragma unroll
     for (int j = 0; j < L::kCopies; ++j)
-      __builtin_amdgcn_global_load_lds(
-          static_cast<const void*>(vt + v_src[j]),
-          (OPL_LDS void*)(st + L::kTile + (wave * L::kCopies + j) * 1024), 16,
-          0, 0);
+      buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave * L::kCopies + j) * 1024,
+                        v_src[j], tile_bytes);
   };
   // K^T-operand rows are l32 (+32 for the second 32-key block, an immediate).
   int k_off[L::kSteps];
@@ -712,7 +737,11 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
 // True when the fp16 fast path applies.
 inline bool f16_dma_ok(const void* q, const void* k, const void* v,
                        const void* out, int sequence, int head_dim) {
+  // one head of K or V must be addressable with 32-bit buffer offsets
+  const unsigned long long head_bytes =
+      static_cast<unsigned long long>(sequence) * head_dim * 2ull;
   return (head_dim == 64 || head_dim == 128) && sequence % kBlockRows == 0 &&
+         head_bytes < (1ull << 32) &&
          opl::aligned16(q) && opl::aligned16(k) && opl::aligned16(v) &&
          opl::aligned16(out);
 }
