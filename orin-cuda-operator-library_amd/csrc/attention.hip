@@ -452,23 +452,6 @@ typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKeys = 64;
 constexpr int kXcds = 8;
-// Word 3 of a raw (untyped, unswizzled) buffer resource on gfx9-family
-// parts: 32-bit data format, no index stride; only the byte range matters.
-constexpr int kBufferFlags = 0x00020000;
-
-// 16 bytes per lane from base + voffset + soffset into LDS at dst + 16 *
-// lane (dst wave-uniform), through a buffer resource over [base, base +
-// bytes): the base lives in scalar registers, offsets past `bytes` read
-// zeros. Kept out of the kernel bodies so the host pass never sees the
-// device-only resource type.
-__device__ __forceinline__ void buffer_copy16_lds(const void* base, unsigned bytes,
-                                                  unsigned char* dst, int voffset,
-                                                  int soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                        bytes, kBufferFlags),
-      (OPL_LDS void*)dst, 16, voffset, soffset, 0, 0);
-}
 // Headroom (log2 units) the running row max may lag the true max by.
 constexpr float kLazyLog2 = 8.0f;
 
@@ -558,11 +541,11 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     const int tile_bytes = key0 * D * 2;
 #pragma unroll
     for (int j = 0; j < L::kCopies; ++j)
-      buffer_copy16_lds(kh, head_bytes, st + (wave * L::kCopies + j) * 1024,
+      opl::buffer_copy16_lds(kh, head_bytes, st + (wave * L::kCopies + j) * 1024,
                         k_src[j], tile_bytes);
 #pragma unroll
     for (int j = 0; j < L::kCopies; ++j)
-      buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave * L::kCopies + j) * 1024,
+      opl::buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave * L::kCopies + j) * 1024,
                         v_src[j], tile_bytes);
   };
   // K^T-operand rows are l32 (+32 for the second 32-key block, an immediate).

@@ -358,31 +358,43 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   const int l32 = lane % 32;
 
   // DMA sources: copy j of this thread fills LDS chunk slot
-  // (wave * kCopies + j) * 64 + lane of each operand tile.
-  const _Float16* a_src[kCopies];
-  const _Float16* b_src[kCopies];
+  // (wave * kCopies + j) * 64 + lane of each operand tile. They are byte
+  // offsets from the step's scalar bases A + m0 * K + k0 and
+  // B + k0 * ldb + n0 (rows clamped to M - 1, columns to ldb - 8), read
+  // through buffer resources: no 64-bit vector address math per copy.
+  int a_dma[kCopies];
+  int b_dma[kCopies];
 #pragma unroll
   for (int j = 0; j < kCopies; ++j) {
     const int slot = (wave * kCopies + j) * 64 + lane;
     const int m = slot / 8;
     const int chunk = (slot % 8) ^ swizzle_a(m);
-    a_src[j] = A + static_cast<std::size_t>(min(m0 + m, M - 1)) * K + 8 * chunk;
+    a_dma[j] = (min(m0 + m, M - 1) - m0) * K * 2 + 16 * chunk;
     const int kk = (wave * kCopies + j) * 2 + lane / 32;
     const int col = n0 + 8 * ((lane % 32) ^ swizzle_b(kk));
-    b_src[j] = B + static_cast<std::size_t>(kk) * ldb + min(col, ldb - 8);
+    b_dma[j] = kk * ldb * 2 + (min(col, ldb - 8) - n0) * 2;
   }
+  // Bytes from each step's base to the end of its operand, capped at the
+  // 32-bit range (every offset above stays far below it).
+  auto span = [](long long bytes) {
+    return static_cast<unsigned>(bytes < 0xffffffffLL ? bytes : 0xffffffffLL);
+  };
   auto issue = [&](unsigned char* stage, int k0) {
     unsigned char* sb = stage + kABytes;
+    const _Float16* a_base = A + static_cast<std::size_t>(m0) * K + k0;
+    const _Float16* b_base = B + static_cast<std::size_t>(k0) * ldb + n0;
+    const unsigned a_span =
+        span((static_cast<long long>(M - m0) * K - k0) * 2);
+    const unsigned b_span =
+        span((static_cast<long long>(K - k0) * ldb - n0) * 2);
 #pragma unroll
     for (int j = 0; j < kCopies; ++j)
-      __builtin_amdgcn_global_load_lds(
-          static_cast<const void*>(a_src[j] + k0),
-          (OPL_LDS void*)(stage + (wave * kCopies + j) * 1024), 16, 0, 0);
+      opl::buffer_copy16_lds(a_base, a_span, stage + (wave * kCopies + j) * 1024,
+                             a_dma[j], 0);
 #pragma unroll
     for (int j = 0; j < kCopies; ++j)
-      __builtin_amdgcn_global_load_lds(
-          static_cast<const void*>(b_src[j] + static_cast<std::size_t>(k0) * ldb),
-          (OPL_LDS void*)(sb + (wave * kCopies + j) * 1024), 16, 0, 0);
+      opl::buffer_copy16_lds(b_base, b_span, sb + (wave * kCopies + j) * 1024,
+                             b_dma[j], 0);
   };
 
   // Fragment byte offsets inside a stage for each of the 4 k16 steps.
