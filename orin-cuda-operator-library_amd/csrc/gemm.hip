@@ -351,7 +351,8 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   const int n0 = tn * kBN;
 
   const int lane = threadIdx.x % opl::kWaveSize;
-  const int wave = threadIdx.x / opl::kWaveSize;
+  // wave-uniform, so each copy's LDS destination is a scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / opl::kWaveSize);
   const int wm = wave / kWN;
   const int wn = wave % kWN;
   const int half = lane / 32;
