@@ -1,0 +1,117 @@
+"""Serving-side behaviour of the launchers (GPU).
+
+* HIP graph capture: every operator, called through torch.ops on the
+  capturing stream, is recorded into one graph; the graph is replayed
+  several times with eager work and synchronizations between replays, and
+  every replay must reproduce the eager results bit for bit (the launchers
+  allocate nothing after their first call on a stream and record no memset
+  nodes).
+* Concurrency: two host threads launch on two streams at once; both get the
+  results a single thread gets (the launchers are reentrant, and library
+  scratch is per stream).
+"""
+
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(device):
+    g = torch.Generator(device="cpu").manual_seed(7)
+    mk = lambda *shape, dtype=torch.float32: torch.randn(*shape, generator=g).to(device, dtype)
+    return {
+        "x": mk(1_000_003),
+        "sm": mk(300, 1003) * 3,
+        "tr": mk(520, 260),
+        "rn": mk(257, 4096),
+        "w": mk(4096).abs() + 0.5,
+        "a": mk(300, 640), "b": mk(640, 512),
+        "ah": mk(1000, 1000, dtype=torch.float16), "bh": mk(1000, 1000, dtype=torch.float16),
+        "a1": mk(1, 4096, dtype=torch.float16), "b1": mk(4096, 4096, dtype=torch.float16),
+        "q": mk(1, 4, 256, 128, dtype=torch.float16),
+        "k": mk(1, 4, 256, 128, dtype=torch.float16),
+        "v": mk(1, 4, 256, 128, dtype=torch.float16),
+    }
+
+
+def _all_ops(ops, t):
+    return [
+        ops.reduce_sum(t["x"]),
+        ops.softmax(t["sm"]),
+        ops.transpose(t["tr"]),
+        ops.rmsnorm(t["rn"], t["w"], 1e-6),
+        ops.gemm(t["a"], t["b"]),
+        ops.gemm(t["ah"], t["bh"]),      # zero-padded workspace path
+        ops.gemm(t["a1"], t["b1"]),      # skinny path with K splits
+        ops.attention(t["q"], t["k"], t["v"], True),
+    ]
+
+
+def test_graph_capture_replays_match_eager(ops, device):
+    t = _inputs(device)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        eager = [y.clone() for y in _all_ops(ops, t)]  # also first use of scratch
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        outs = _all_ops(ops, t)
+    for replay in range(4):
+        for y in outs:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (y, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(y, e), (replay, i)
+        # eager work on the same buffers' neighbours between replays
+        _ = ops.softmax(t["sm"] * 0.5)
+        torch.cuda.synchronize()
+
+
+def test_two_threads_two_streams(ops, device):
+    t = _inputs(device)
+    with torch.cuda.stream(torch.cuda.Stream()):
+        single = [y.clone() for y in _all_ops(ops, t)]
+    torch.cuda.synchronize()
+    results, errors = {}, []
+
+    def worker(name):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                out = None
+                for _ in range(5):
+                    out = _all_ops(ops, t)
+            s.synchronize()
+            results[name] = [y.clone() for y in out]
+        except Exception as exc:  # reported below
+            errors.append(repr(exc))
+
+    threads = [threading.Thread(target=worker, args=(n,)) for n in ("t0", "t1")]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not errors, errors
+    for name in ("t0", "t1"):
+        for i, (y, e) in enumerate(zip(results[name], single)):
+            assert torch.equal(y, e), (name, i)
+
+
+def test_eager_results_match_oracle_spot_check(ops, device):
+    """Anchor the bit-for-bit comparisons above to the oracle."""
+    t = _inputs(device)
+    y = ops.softmax(t["sm"]).cpu().numpy()
+    assert np.max(np.abs(y - oracle.softmax(t["sm"].cpu().numpy()))) <= 1e-6
+    r = ops.reduce_sum(t["x"]).item()
+    ref = oracle.reduce_sum(t["x"].cpu().numpy())
+    assert abs(r - ref) <= 1e-5 * max(abs(ref), 1.0)
