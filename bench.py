@@ -277,6 +277,33 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         out.append(bw_entry(name, list(shape), nb, *time_single(torch, f, steps, warmup), ref))
         del xs
 
+    # FP16 rows (fp32 arithmetic inside): the reference's deferred dtype
+    # extension, so no Orin figure; same shapes as the fp32 configs.
+    for name, shape in (("softmax_f16", (4096, 1024)), ("softmax_f16", (4097, 1023))):
+        if not want("softmax"):
+            break
+        x = torch.from_numpy(oracle.normal(22, shape, 0.0, 3.0)).half()
+        nb = 2 * 2 * shape[0] * shape[1]
+        sets = sets_for(nb)
+        xs = [(x.cuda(), torch.empty(shape, device=dev, dtype=torch.float16)) for _ in range(sets)]
+        f = lambda i: lib.operatorlib_softmax_f16(ptr(xs[i % sets][0]), ptr(xs[i % sets][1]),
+                                                  shape[0], shape[1], stream)
+        out.append(bw_entry(name, list(shape), nb, *time_single(torch, f, steps, warmup)))
+        del xs
+
+    for name, shape in (("rmsnorm_f16", (2048, 4096)), ("rmsnorm_f16", (2047, 4095))):
+        if not want("rmsnorm"):
+            break
+        x = torch.from_numpy(oracle.normal(23, shape)).half()
+        w = torch.from_numpy(oracle.uniform(24, shape[1], 0.5, 1.5)).half().cuda()
+        nb = (2 * shape[0] * shape[1] + shape[1]) * 2
+        sets = sets_for(nb)
+        xs = [(x.cuda(), torch.empty(shape, device=dev, dtype=torch.float16)) for _ in range(sets)]
+        f = lambda i: lib.operatorlib_rmsnorm_f16(ptr(xs[i % sets][0]), ptr(w), ptr(xs[i % sets][1]),
+                                                  shape[0], shape[1], 1e-6, stream)
+        out.append(bw_entry(name, list(shape), nb, *time_single(torch, f, steps, warmup)))
+        del xs
+
     for name, shape, ref in (("transpose_f32", (4096, 4096), 94.34), ("transpose_f32", (4095, 4097), None)):
         if not want("transpose"):
             break

@@ -73,6 +73,30 @@ int operatorlib_rmsnorm_f32(const float* input, const float* weight,
                             float epsilon, void* stream);
 
 /*
+ * softmax_f32 for fp16 rows: fp16 input and output, max / exp / sum in
+ * fp32, each output rounded to fp16 once (round to nearest even).
+ * Errors: as operatorlib_softmax_f32.
+ * No entry point in the reference: its deferred "FP16 input, FP32
+ * accumulation" extension (docs/pytorch_extension.md:143-146,
+ * softmax/reports/v4.md:140-141).
+ */
+int operatorlib_softmax_f16(const operatorlib_half_t* input,
+                            operatorlib_half_t* output, int rows, int cols,
+                            void* stream);
+
+/*
+ * rmsnorm_f32 for fp16 tensors: fp16 input, weight and output; the sum of
+ * squares, rsqrt and scaling in fp32, each output rounded to fp16 once.
+ * Errors: as operatorlib_rmsnorm_f32.
+ * No entry point in the reference: its deferred FP16 extension
+ * (docs/pytorch_extension.md:143-146).
+ */
+int operatorlib_rmsnorm_f16(const operatorlib_half_t* input,
+                            const operatorlib_half_t* weight,
+                            operatorlib_half_t* output, int tokens,
+                            int hidden, float epsilon, void* stream);
+
+/*
  * Row-major C[m, n] = A[m, k] * B[k, n], fp32 in / fp32 out.
  * Errors: NULL pointer, m/n/k <= 0.
  * Replaces operatorlib::gemm_f32, reference src/gemm.cu:440-453.

@@ -49,6 +49,28 @@ inline hipError_t rmsnorm_f32(const float* input, const float* weight,
       static_cast<void*>(stream)));
 }
 
+// FP16 rows, FP32 max / exp / sum, FP16 output. Not in the reference API
+// (its deferred FP16 extension, docs/pytorch_extension.md:143-146).
+inline hipError_t softmax_f16(const __half* input, __half* output, int rows,
+                              int cols, hipStream_t stream = nullptr) {
+  return static_cast<hipError_t>(operatorlib_softmax_f16(
+      reinterpret_cast<const operatorlib_half_t*>(input),
+      reinterpret_cast<operatorlib_half_t*>(output), rows, cols,
+      static_cast<void*>(stream)));
+}
+
+// FP16 input / weight / output, FP32 sum of squares and scaling. Not in the
+// reference API (its deferred FP16 extension).
+inline hipError_t rmsnorm_f16(const __half* input, const __half* weight,
+                              __half* output, int tokens, int hidden,
+                              float epsilon, hipStream_t stream = nullptr) {
+  return static_cast<hipError_t>(operatorlib_rmsnorm_f16(
+      reinterpret_cast<const operatorlib_half_t*>(input),
+      reinterpret_cast<const operatorlib_half_t*>(weight),
+      reinterpret_cast<operatorlib_half_t*>(output), tokens, hidden, epsilon,
+      static_cast<void*>(stream)));
+}
+
 // Row-major C[M,N] = A[M,K] * B[K,N].
 // Reference: include/operatorlib/operators.h:27
 inline hipError_t gemm_f32(const float* a, const float* b, float* c, int m,

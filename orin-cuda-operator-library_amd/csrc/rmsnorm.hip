@@ -1,4 +1,7 @@
-// rmsnorm_f32: y[t, h] = x[t, h] * rsqrt(mean_h(x[t, :]^2) + eps) * w[h].
+// rmsnorm_f32 / rmsnorm_f16: y[t, h] = x[t, h] * rsqrt(mean_h(x[t, :]^2) +
+// eps) * w[h]. The fp16 variant (fp16 x, w and y) computes in fp32 and
+// rounds y to fp16 once, on store: the "FP16 input, FP32 accumulation"
+// extension the reference defers (docs/pytorch_extension.md:143-146).
 //
 // Reference: operatorlib::rmsnorm_f32 (src/rmsnorm.cu:77-95, kernels :27-71).
 // Its kernels read x twice (once for the sum of squares, once to scale).
@@ -7,9 +10,9 @@
 //
 // MI355X design: a single fused pass. The row is held in VGPRs (one
 // wavefront per row up to 4096 columns, one 512-thread workgroup per row up
-// to 32768), so x is read from HBM once and y written once; w (hidden * 4
+// to 32768), so x is read from HBM once and y written once; w (one row of
 // bytes) is shared by all rows and served from L2/MALL after first touch.
-// Algorithmic traffic: (2 * tokens * hidden + hidden) * 4 bytes.
+// Algorithmic traffic: (2 * tokens * hidden + hidden) * sizeof(element).
 // Only rows longer than 32768 columns re-read x (two passes).
 
 #include <hip/hip_runtime.h>
@@ -31,40 +34,40 @@ __device__ __forceinline__ float sum_squares(const float (&x)[N]) {
   return s;
 }
 
-template <int V, int Lanes, int W>
+template <int V, int Lanes, int W, typename T>
 __device__ __forceinline__ void scale_store(
-    opl::RowSlice<V, Lanes, W>& s, const float* __restrict__ weight,
-    float* __restrict__ out_row, int cols, int t, float inv) {
-  opl::RowSlice<V, Lanes, W> w;
+    opl::RowSlice<V, Lanes, W, T>& s, const T* __restrict__ weight,
+    T* __restrict__ out_row, int cols, int t, float inv) {
+  opl::RowSlice<V, Lanes, W, T> w;
   w.load(weight, cols, t, 0.0f);
 #pragma unroll
-  for (int i = 0; i < opl::RowSlice<V, Lanes, W>::kCount; ++i)
+  for (int i = 0; i < opl::RowSlice<V, Lanes, W, T>::kCount; ++i)
     s.x[i] = (s.x[i] * inv) * w.x[i];
   s.store(out_row, cols, t);
 }
 
-template <int V, int W>
+template <typename T, int V, int W>
 __global__ __launch_bounds__(opl::kRowWaveThreads) void rmsnorm_wave_kernel(
-    const float* __restrict__ input, const float* __restrict__ weight,
-    float* __restrict__ output, int rows, int cols, float epsilon) {
+    const T* __restrict__ input, const T* __restrict__ weight,
+    T* __restrict__ output, int rows, int cols, float epsilon) {
   const int lane = threadIdx.x % opl::kWaveSize;
   const int row = blockIdx.x * opl::kRowWaveRows + threadIdx.x / opl::kWaveSize;
   if (row >= rows) return;  // uniform per wavefront
   const std::size_t offset = static_cast<std::size_t>(row) * cols;
-  opl::RowSlice<V, opl::kWaveSize, W> s;
+  opl::RowSlice<V, opl::kWaveSize, W, T> s;
   s.load(input + offset, cols, lane, 0.0f);
   const float ss = opl::wave_reduce<opl::SumOp>(sum_squares(s.x));
   const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
   scale_store(s, weight, output + offset, cols, lane, inv);
 }
 
-template <int V, int W>
+template <typename T, int V, int W>
 __global__ __launch_bounds__(opl::kRowBlockThreads) void rmsnorm_block_kernel(
-    const float* __restrict__ input, const float* __restrict__ weight,
-    float* __restrict__ output, int cols, float epsilon) {
+    const T* __restrict__ input, const T* __restrict__ weight,
+    T* __restrict__ output, int cols, float epsilon) {
   __shared__ float slots[opl::kRowBlockWaves];
   const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
-  opl::RowSlice<V, opl::kRowBlockThreads, W> s;
+  opl::RowSlice<V, opl::kRowBlockThreads, W, T> s;
   s.load(input + offset, cols, threadIdx.x, 0.0f);
   const float ss = opl::block_reduce<opl::SumOp, opl::kRowBlockWaves>(
       sum_squares(s.x), slots);
@@ -72,39 +75,50 @@ __global__ __launch_bounds__(opl::kRowBlockThreads) void rmsnorm_block_kernel(
   scale_store(s, weight, output + offset, cols, threadIdx.x, inv);
 }
 
-// Ragged rows (hidden % 4 != 0 or unaligned; input and output rows in the
-// same 16-byte phase): x and y move as float4 bodies plus scalar head/tail.
-// Rows of one launch start at different offsets modulo 16 bytes, so w is
-// read per element: from LDS in the wavefront kernel (staged once per
-// workgroup of 4 rows), from L2 in the workgroup kernel.
-template <int V, int Lanes, typename WeightAt>
+// Ragged rows (hidden % E != 0 or unaligned; input and output rows in the
+// same 16-byte phase): x and y move as 16-byte chunk bodies plus scalar
+// head/tail. Rows of one launch start at different offsets modulo 16 bytes,
+// so w is read per element: from LDS in the wavefront kernel (staged once
+// per workgroup of 4 rows), from L2 in the workgroup kernel.
+template <int V, int Lanes, typename T, typename WeightAt>
 __device__ __forceinline__ void ragged_scale_store(
-    opl::RaggedRowSlice<V, Lanes>& s, WeightAt w, float* __restrict__ out_row,
+    opl::RaggedRowSlice<V, Lanes, T>& s, WeightAt w, T* __restrict__ out_row,
     int cols, int t, float inv) {
+  constexpr int E = opl::RaggedRowSlice<V, Lanes, T>::kE;
+  // All weight reads issue before the first use (clamped to column 0 for
+  // slots outside the row, whose results store() never writes).
+  float wv[E * V + 1];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    if (j * Lanes + t < s.body) {
+    const bool in = j * Lanes + t < s.body;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        s.x[4 * j + e] = (s.x[4 * j + e] * inv) * w(s.body_col(t, 4 * j + e));
-    }
+    for (int e = 0; e < E; ++e) wv[E * j + e] = w(in ? s.body_col(t, E * j + e) : 0);
   }
   const int c = s.extra_col(t, cols);
-  if (c >= 0) s.x[4 * V] = (s.x[4 * V] * inv) * w(c);
+  wv[E * V] = w(c >= 0 ? c : 0);
+#pragma unroll
+  for (int i = 0; i < E * V + 1; ++i) s.x[i] = (s.x[i] * inv) * wv[i];
   s.store(out_row, cols, t);
 }
 
-// Copy s (0-3) of the staged weights holds w[c] at float index c + s, so a
-// row whose float4 body starts at column `head` reads its weights as
-// aligned float4s from copy (4 - head) % 4: conflict-free ds_read_b128
-// instead of four 4-byte reads at a 16-byte lane stride.
-constexpr int kWeightCopyPitch = opl::kRowWaveMaxCols + 4;
+// The wavefront kernel stages E shifted copies of the weights (E elements
+// per 16-byte chunk): copy s holds w[c] at element index c + s, so a row
+// whose chunk body starts at column `head` reads its weights as aligned
+// 16-byte chunks from copy (E - head) % E: conflict-free ds_read_b128
+// instead of E narrow reads at a 16-byte lane stride.
+template <typename T>
+constexpr int weight_copy_pitch() {
+  return opl::kRowWaveMaxCols + opl::RowElem<T>::kPerChunk;
+}
 
-template <int V>
+template <typename T, int V>
 __global__ __launch_bounds__(opl::kRowWaveThreads) void rmsnorm_ragged_wave_kernel(
-    const float* __restrict__ input, const float* __restrict__ weight,
-    float* __restrict__ output, int rows, int cols, float epsilon) {
-  __shared__ __attribute__((aligned(16))) float w_lds[4 * kWeightCopyPitch];
+    const T* __restrict__ input, const T* __restrict__ weight,
+    T* __restrict__ output, int rows, int cols, float epsilon) {
+  using Chunk = typename opl::RowElem<T>::Chunk;
+  constexpr int E = opl::RowElem<T>::kPerChunk;
+  constexpr int kPitch = weight_copy_pitch<T>();
+  __shared__ __attribute__((aligned(16))) T w_lds[E * kPitch];
   const int lane = threadIdx.x % opl::kWaveSize;
   const int row = blockIdx.x * opl::kRowWaveRows + threadIdx.x / opl::kWaveSize;
   const bool active = row < rows;  // uniform per wavefront
@@ -113,115 +127,158 @@ __global__ __launch_bounds__(opl::kRowWaveThreads) void rmsnorm_ragged_wave_kern
   // LDS writes of the weights wait only for the older weight loads and the
   // row's HBM latency overlaps the staging and its barrier.
   constexpr int kWPerThread = opl::kRowWaveMaxCols / opl::kRowWaveThreads;
-  float wv[kWPerThread];
+  T wv[kWPerThread];
 #pragma unroll
   for (int i = 0; i < kWPerThread; ++i) {
     const int c = static_cast<int>(threadIdx.x) + opl::kRowWaveThreads * i;
     wv[i] = weight[c < cols ? c : cols - 1];
   }
-  opl::RaggedRowSlice<V, opl::kWaveSize> s;
+  opl::RaggedRowSlice<V, opl::kWaveSize, T> s;
   s.load_raw(input + offset, cols, lane);  // row 0 stands in for inactive waves
   __builtin_amdgcn_sched_barrier(0);       // keep the row's loads in flight
   // Every slot written (those at or past `cols` repeat the last weight and
   // are never read), so the writes need no branches.
 #pragma unroll
-  for (int copy = 0; copy < 4; ++copy)
+  for (int copy = 0; copy < E; ++copy)
 #pragma unroll
     for (int i = 0; i < kWPerThread; ++i)
-      w_lds[copy * kWeightCopyPitch + copy + static_cast<int>(threadIdx.x) +
+      w_lds[copy * kPitch + copy + static_cast<int>(threadIdx.x) +
             opl::kRowWaveThreads * i] = wv[i];
   __syncthreads();
   if (!active) return;
   s.mask(cols, lane, 0.0f);
   const float ss = opl::wave_reduce<opl::SumOp>(sum_squares(s.x));
   const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
-  const int copy = (4 - s.head) & 3;
-  const float4* w4 = reinterpret_cast<const float4*>(
-      w_lds + copy * kWeightCopyPitch + copy + s.head);  // 16-byte aligned
+  const int copy = (E - s.head) & (E - 1);
+  const Chunk* wc = reinterpret_cast<const Chunk*>(
+      w_lds + copy * kPitch + copy + s.head);  // 16-byte aligned
 #pragma unroll
   for (int j = 0; j < V; ++j) {
     const int q = j * opl::kWaveSize + lane;
-    const float4 wq = w4[q < s.body ? q : 0];
-    s.x[4 * j + 0] = (s.x[4 * j + 0] * inv) * wq.x;
-    s.x[4 * j + 1] = (s.x[4 * j + 1] * inv) * wq.y;
-    s.x[4 * j + 2] = (s.x[4 * j + 2] * inv) * wq.z;
-    s.x[4 * j + 3] = (s.x[4 * j + 3] * inv) * wq.w;
+    const Chunk wq = wc[q < s.body ? q : 0];
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      s.x[E * j + e] = (s.x[E * j + e] * inv) * static_cast<float>(wq[e]);
   }
   const int c = s.extra_col(lane, cols);
-  s.x[4 * V] = (s.x[4 * V] * inv) * w_lds[c >= 0 ? c : 0];
+  s.x[E * V] = (s.x[E * V] * inv) * static_cast<float>(w_lds[c >= 0 ? c : 0]);
   s.store(output + offset, cols, lane);
 }
 
-template <int V>
+template <typename T, int V>
 __global__ __launch_bounds__(opl::kRowBlockThreads) void rmsnorm_ragged_block_kernel(
-    const float* __restrict__ input, const float* __restrict__ weight,
-    float* __restrict__ output, int cols, float epsilon) {
+    const T* __restrict__ input, const T* __restrict__ weight,
+    T* __restrict__ output, int cols, float epsilon) {
   __shared__ float slots[opl::kRowBlockWaves];
   const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
-  opl::RaggedRowSlice<V, opl::kRowBlockThreads> s;
+  opl::RaggedRowSlice<V, opl::kRowBlockThreads, T> s;
   s.load(input + offset, cols, threadIdx.x, 0.0f);
   const float ss = opl::block_reduce<opl::SumOp, opl::kRowBlockWaves>(
       sum_squares(s.x), slots);
   const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
-  ragged_scale_store(s, [&](int c) { return weight[c]; }, output + offset,
-                     cols, threadIdx.x, inv);
+  ragged_scale_store(
+      s, [&](int c) { return static_cast<float>(weight[c]); },
+      output + offset, cols, threadIdx.x, inv);
 }
 
+template <typename T>
 __global__ __launch_bounds__(opl::kRowBlockThreads) void rmsnorm_two_pass_kernel(
-    const float* __restrict__ input, const float* __restrict__ weight,
-    float* __restrict__ output, int cols, float epsilon) {
+    const T* __restrict__ input, const T* __restrict__ weight,
+    T* __restrict__ output, int cols, float epsilon) {
   __shared__ float slots[opl::kRowBlockWaves];
   const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
-  const float* row = input + offset;
-  float* out = output + offset;
+  const T* row = input + offset;
+  T* out = output + offset;
   float ss = 0.0f;
-  for (int c = threadIdx.x; c < cols; c += opl::kRowBlockThreads)
-    ss += row[c] * row[c];
+  for (int c = threadIdx.x; c < cols; c += opl::kRowBlockThreads) {
+    const float x = static_cast<float>(row[c]);
+    ss += x * x;
+  }
   ss = opl::block_reduce<opl::SumOp, opl::kRowBlockWaves>(ss, slots);
   const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
   for (int c = threadIdx.x; c < cols; c += opl::kRowBlockThreads)
-    out[c] = (row[c] * inv) * weight[c];
+    out[c] = static_cast<T>((static_cast<float>(row[c]) * inv) *
+                            static_cast<float>(weight[c]));
 }
 
+template <typename T>
 struct Args {
-  const float* input;
-  const float* weight;
-  float* output;
+  const T* input;
+  const T* weight;
+  T* output;
   int rows;
   int cols;
   float epsilon;
 };
 
-// W: 4 aligned float4 rows, 1 element-wise, 0 ragged float4 rows.
-template <int W, int V, int MaxV>
-void launch_wave(int v, const Args& a, hipStream_t stream) {
+// W: E aligned 16-byte chunks, 1 element-wise, 0 ragged chunk rows.
+template <typename T, int W, int V, int MaxV>
+void launch_wave(int v, const Args<T>& a, hipStream_t stream) {
   if constexpr (V < MaxV) {
-    if (v > V) return launch_wave<W, 2 * V, MaxV>(v, a, stream);
+    if (v > V) return launch_wave<T, W, 2 * V, MaxV>(v, a, stream);
   }
   const int blocks = (a.rows + opl::kRowWaveRows - 1) / opl::kRowWaveRows;
   if constexpr (W == 0)
-    rmsnorm_ragged_wave_kernel<V><<<dim3(blocks), dim3(opl::kRowWaveThreads), 0,
-                                    stream>>>(a.input, a.weight, a.output,
-                                              a.rows, a.cols, a.epsilon);
+    rmsnorm_ragged_wave_kernel<T, V><<<dim3(blocks), dim3(opl::kRowWaveThreads),
+                                       0, stream>>>(a.input, a.weight, a.output,
+                                                    a.rows, a.cols, a.epsilon);
   else
-    rmsnorm_wave_kernel<V, W><<<dim3(blocks), dim3(opl::kRowWaveThreads), 0,
-                                stream>>>(a.input, a.weight, a.output, a.rows,
-                                          a.cols, a.epsilon);
+    rmsnorm_wave_kernel<T, V, W><<<dim3(blocks), dim3(opl::kRowWaveThreads), 0,
+                                   stream>>>(a.input, a.weight, a.output, a.rows,
+                                             a.cols, a.epsilon);
 }
 
-template <int W, int V, int MaxV>
-void launch_block(int v, const Args& a, hipStream_t stream) {
+template <typename T, int W, int V, int MaxV>
+void launch_block(int v, const Args<T>& a, hipStream_t stream) {
   if constexpr (V < MaxV) {
-    if (v > V) return launch_block<W, 2 * V, MaxV>(v, a, stream);
+    if (v > V) return launch_block<T, W, 2 * V, MaxV>(v, a, stream);
   }
   if constexpr (W == 0)
-    rmsnorm_ragged_block_kernel<V><<<dim3(a.rows),
-                                     dim3(opl::kRowBlockThreads), 0, stream>>>(
+    rmsnorm_ragged_block_kernel<T, V><<<dim3(a.rows),
+                                        dim3(opl::kRowBlockThreads), 0, stream>>>(
         a.input, a.weight, a.output, a.cols, a.epsilon);
   else
-    rmsnorm_block_kernel<V, W><<<dim3(a.rows),
-                                 dim3(opl::kRowBlockThreads), 0, stream>>>(
+    rmsnorm_block_kernel<T, V, W><<<dim3(a.rows),
+                                    dim3(opl::kRowBlockThreads), 0, stream>>>(
         a.input, a.weight, a.output, a.cols, a.epsilon);
+}
+
+// Shared dispatch of the fp32 and fp16 entry points (E elements per 16-byte
+// chunk; per-thread counts as in softmax).
+template <typename T>
+int rmsnorm_launch(const Args<T>& args, hipStream_t stream) {
+  constexpr int E = opl::RowElem<T>::kPerChunk;
+  constexpr int kWaveMaxV = opl::kRowWaveMaxCols / (opl::kWaveSize * E);
+  constexpr int kBlockMinV =
+      2 * opl::kRowWaveMaxCols / (opl::kRowBlockThreads * E);
+  constexpr int kBlockMaxV =
+      opl::kRowBlockMaxCols / (opl::kRowBlockThreads * E);
+  const int hidden = args.cols;
+  const bool vec = hidden % E == 0 && opl::aligned16(args.input) &&
+                   opl::aligned16(args.weight) && opl::aligned16(args.output);
+  const bool ragged =
+      !vec && opl::same_phase16(args.input, args.output) &&
+      hidden >= opl::RaggedRowSlice<1, opl::kWaveSize, T>::kMinCols;
+  const opl::RowPlan plan = opl::pick_row_plan(hidden, vec || ragged ? E : 1);
+  switch (plan.path) {
+    case opl::RowPath::kWave:
+      if (vec) launch_wave<T, E, 1, kWaveMaxV>(plan.per_thread, args, stream);
+      else if (ragged) launch_wave<T, 0, 1, kWaveMaxV>(plan.per_thread, args, stream);
+      else launch_wave<T, 1, 1, 64>(plan.per_thread, args, stream);
+      break;
+    case opl::RowPath::kBlock:
+      if (vec) launch_block<T, E, kBlockMinV, kBlockMaxV>(plan.per_thread, args, stream);
+      else if (ragged) launch_block<T, 0, kBlockMinV, kBlockMaxV>(plan.per_thread, args, stream);
+      else launch_block<T, 1, 16, 64>(plan.per_thread, args, stream);
+      break;
+    case opl::RowPath::kTwoPass:
+      rmsnorm_two_pass_kernel<T><<<dim3(args.rows), dim3(opl::kRowBlockThreads),
+                                   0, stream>>>(args.input, args.weight,
+                                                args.output, hidden,
+                                                args.epsilon);
+      break;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -231,29 +288,22 @@ extern "C" int operatorlib_rmsnorm_f32(const float* input, const float* weight,
                                        float epsilon, void* stream_handle) {
   if (!opl::rmsnorm_args_ok(input, weight, output, tokens, hidden, epsilon))
     return hipErrorInvalidValue;
-  hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-  const bool vec4 = hidden % 4 == 0 && opl::aligned16(input) &&
-                    opl::aligned16(weight) && opl::aligned16(output);
-  const bool ragged = !vec4 && opl::same_phase16(input, output) &&
-                      hidden >= opl::kRaggedMinCols;
-  const Args args{input, weight, output, tokens, hidden, epsilon};
-  const opl::RowPlan plan = opl::pick_row_plan(hidden, vec4 || ragged);
-  switch (plan.path) {
-    case opl::RowPath::kWave:
-      if (vec4) launch_wave<4, 1, 16>(plan.per_thread, args, stream);
-      else if (ragged) launch_wave<0, 1, 16>(plan.per_thread, args, stream);
-      else launch_wave<1, 1, 64>(plan.per_thread, args, stream);
-      break;
-    case opl::RowPath::kBlock:
-      if (vec4) launch_block<4, 4, 16>(plan.per_thread, args, stream);
-      else if (ragged) launch_block<0, 4, 16>(plan.per_thread, args, stream);
-      else launch_block<1, 16, 64>(plan.per_thread, args, stream);
-      break;
-    case opl::RowPath::kTwoPass:
-      rmsnorm_two_pass_kernel<<<dim3(tokens), dim3(opl::kRowBlockThreads), 0,
-                                stream>>>(input, weight, output, hidden,
-                                          epsilon);
-      break;
-  }
-  return hipGetLastError();
+  return rmsnorm_launch(
+      Args<float>{input, weight, output, tokens, hidden, epsilon},
+      static_cast<hipStream_t>(stream_handle));
+}
+
+extern "C" int operatorlib_rmsnorm_f16(const operatorlib_half_t* input,
+                                       const operatorlib_half_t* weight,
+                                       operatorlib_half_t* output, int tokens,
+                                       int hidden, float epsilon,
+                                       void* stream_handle) {
+  if (!opl::rmsnorm_args_ok(input, weight, output, tokens, hidden, epsilon))
+    return hipErrorInvalidValue;
+  return rmsnorm_launch(
+      Args<_Float16>{reinterpret_cast<const _Float16*>(input),
+                     reinterpret_cast<const _Float16*>(weight),
+                     reinterpret_cast<_Float16*>(output), tokens, hidden,
+                     epsilon},
+      static_cast<hipStream_t>(stream_handle));
 }

@@ -3,14 +3,16 @@
 // RMSNorm).
 //
 // A row is owned by a group of `Lanes` threads (one wavefront, or a whole
-// workgroup for long rows). Thread t of the group holds the row's elements
-//   W == 4:  float4 number  j * Lanes + t   (16-byte loads/stores; needs
-//            cols % 4 == 0 and 16-byte aligned base pointers)
-//   W == 1:  element        j * Lanes + t   (4-byte accesses; any shape)
+// workgroup for long rows). Rows are stored as fp32 or fp16 (T) and held
+// in VGPRs as fp32. Thread t of the group holds the row's elements
+//   W == E:  16-byte chunk  j * Lanes + t   (E = 4 fp32 or 8 fp16 elements;
+//            needs cols % E == 0 and 16-byte aligned base pointers)
+//   W == 1:  element        j * Lanes + t   (any shape)
 // for j = 0 .. V-1; RaggedRowSlice (below) keeps 16-byte accesses for rows
-// of any length and alignment. Consecutive lanes touch consecutive addresses, so every
-// wave-wide access is one contiguous 256 B (W=1) or 1 KiB (W=4) segment.
-// The whole row is read from HBM exactly once and written exactly once.
+// of any length and alignment. Consecutive lanes touch consecutive
+// addresses, so every wave-wide access is one contiguous segment (1 KiB for
+// 16-byte chunks). The whole row is read from HBM exactly once and written
+// exactly once.
 //
 // Launch shapes (chosen by pick_row_plan):
 //   cols <= 4096   one wavefront per row, 4 rows per 256-thread workgroup
@@ -32,8 +34,25 @@ constexpr int kRowBlockWaves = kRowBlockThreads / kWaveSize;
 constexpr int kRowWaveMaxCols = 4096;
 constexpr int kRowBlockMaxCols = 32768;
 
-template <int V, int Lanes, int W>
+// Storage formats of a row. Rows are kept in VGPRs as fp32 whatever the
+// storage type; Chunk is one 16-byte access (4 fp32 or 8 fp16 elements).
+template <typename T>
+struct RowElem;
+template <>
+struct RowElem<float> {
+  typedef float Chunk __attribute__((ext_vector_type(4)));
+  static constexpr int kPerChunk = 4;
+};
+template <>
+struct RowElem<_Float16> {
+  typedef _Float16 Chunk __attribute__((ext_vector_type(8)));
+  static constexpr int kPerChunk = 8;
+};
+
+template <int V, int Lanes, int W, typename T = float>
 struct RowSlice {
+  using Chunk = typename RowElem<T>::Chunk;
+  static_assert(W == 1 || W == RowElem<T>::kPerChunk, "access width");
   static constexpr int kCount = V * W;
   float x[kCount];
 
@@ -41,35 +60,52 @@ struct RowSlice {
     return (j * Lanes + t) * W;
   }
 
-  __device__ __forceinline__ void load(const float* __restrict__ row,
-                                       int cols, int t, float pad) {
+  // Every load is issued from a clamped index (element / chunk 0 always
+  // exists: cols >= W), and out-of-row slots are replaced afterwards. A
+  // load inside a per-slot branch makes the compiler wait for it inside the
+  // branch (s_waitcnt vmcnt(0) per slot), serialising the row's loads.
+  __device__ __forceinline__ void load(const T* __restrict__ row, int cols,
+                                       int t, float pad) {
+    if constexpr (W > 1) {
+      Chunk q[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const int c = first_col(t, j);
-      if constexpr (W == 4) {
-        float4 q = make_float4(pad, pad, pad, pad);
-        if (c < cols) q = *reinterpret_cast<const float4*>(row + c);
-        x[4 * j + 0] = q.x;
-        x[4 * j + 1] = q.y;
-        x[4 * j + 2] = q.z;
-        x[4 * j + 3] = q.w;
-      } else {
-        x[j] = c < cols ? row[c] : pad;
+      for (int j = 0; j < V; ++j) {
+        const int c = first_col(t, j);
+        q[j] = *reinterpret_cast<const Chunk*>(row + (c < cols ? c : 0));
       }
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const bool in = first_col(t, j) < cols;
+#pragma unroll
+        for (int e = 0; e < W; ++e)
+          x[W * j + e] = in ? static_cast<float>(q[j][e]) : pad;
+      }
+    } else {
+      T q[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int c = first_col(t, j);
+        q[j] = row[c < cols ? c : 0];
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        x[j] = first_col(t, j) < cols ? static_cast<float>(q[j]) : pad;
     }
   }
 
-  __device__ __forceinline__ void store(float* __restrict__ row, int cols,
+  __device__ __forceinline__ void store(T* __restrict__ row, int cols,
                                         int t) const {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int c = first_col(t, j);
       if (c < cols) {
-        if constexpr (W == 4) {
-          *reinterpret_cast<float4*>(row + c) =
-              make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+        if constexpr (W > 1) {
+          Chunk q;
+#pragma unroll
+          for (int e = 0; e < W; ++e) q[e] = static_cast<T>(x[W * j + e]);
+          *reinterpret_cast<Chunk*>(row + c) = q;
         } else {
-          row[c] = x[j];
+          row[c] = static_cast<T>(x[j]);
         }
       }
     }
@@ -81,63 +117,65 @@ struct RowSlice {
   }
 };
 
-// A row at any 4-byte alignment and of any length, still moved with
-// 16-byte accesses: a scalar head (the 0-3 elements before the row's first
-// 16-byte boundary), an aligned float4 body, and a scalar tail (< 4
-// elements). Thread t holds body float4s j * Lanes + t (j < V) in x[0, 4V)
-// and at most one head or tail element in x[4V]: threads 0-2 the head,
-// threads 4-6 the tail. Input and output rows must share their offset
-// modulo 16 bytes (the layout is computed once from the input row), and
-// rows must hold at least kRaggedMinCols elements, so the body is never
-// empty.
-constexpr int kRaggedMinCols = 8;
-
-template <int V, int Lanes>
+// A row at any element alignment and of any length, still moved with
+// 16-byte accesses: a scalar head (the 0 to E-1 elements before the row's
+// first 16-byte boundary, E elements per chunk), an aligned chunk body, and
+// a scalar tail (< E elements). Thread t holds body chunks j * Lanes + t
+// (j < V) in x[0, E*V) and at most one head or tail element in x[E*V]:
+// threads 0 .. E-2 the head, threads E .. 2E-2 the tail. Input and output
+// rows must share their offset modulo 16 bytes (the layout is computed once
+// from the input row), and rows must hold at least kMinCols = 2E elements,
+// so the body is never empty.
+template <int V, int Lanes, typename T = float>
 struct RaggedRowSlice {
-  static constexpr int kCount = 4 * V + 1;
+  using Chunk = typename RowElem<T>::Chunk;
+  static constexpr int kE = RowElem<T>::kPerChunk;
+  static_assert(kE == 4 || kE == 8, "chunk of 4 or 8 elements");
+  static constexpr int kMinCols = 2 * kE;
+  static_assert(Lanes >= 2 * kE, "head and tail need 2E lanes");
+  static constexpr int kCount = kE * V + 1;
   float x[kCount];
   int head;        // elements before the first 16-byte boundary
-  int body;        // float4s in the aligned body
-  int tail_start;  // first tail element (head + 4 * body)
+  int body;        // chunks in the aligned body
+  int tail_start;  // first tail element (head + E * body)
 
-  __device__ __forceinline__ void layout(const float* row, int cols) {
-    head = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(row) & 15)) & 15) >> 2);
+  __device__ __forceinline__ void layout(const T* row, int cols) {
+    head = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(row) & 15)) & 15) /
+                            sizeof(T));
     if (head > cols) head = cols;
-    body = (cols - head) >> 2;
-    tail_start = head + 4 * body;
+    body = (cols - head) >> (kE == 8 ? 3 : 2);  // cols - head >= 0
+    tail_start = head + kE * body;
   }
 
-  // Column held in x[4V] by thread t, or -1.
+  // Column held in x[E*V] by thread t, or -1.
   __device__ __forceinline__ int extra_col(int t, int cols) const {
     if (t < head) return t;
-    const int c = tail_start + t - 4;
-    return (t >= 4 && c < cols) ? c : -1;
+    const int c = tail_start + t - kE;
+    return (t >= kE && c < cols) ? c : -1;
   }
 
-  // Column of body slot i (0 <= i < 4V) of thread t; valid if < tail_start.
+  // Column of body slot i (0 <= i < E*V) of thread t; valid if < tail_start.
   __device__ __forceinline__ int body_col(int t, int i) const {
-    return head + 4 * ((i / 4) * Lanes + t) + (i % 4);
+    return head + kE * ((i / kE) * Lanes + t) + (i % kE);
   }
 
   // Loads are unconditional (indices clamped into the row), so they issue
   // back to back without per-load branches: load_raw() only issues them,
   // mask() later replaces the out-of-range slots by `pad` (which waits for
   // the data), and load() does both.
-  __device__ __forceinline__ void load_raw(const float* __restrict__ row,
+  __device__ __forceinline__ void load_raw(const T* __restrict__ row,
                                            int cols, int t) {
     layout(row, cols);
-    const float4* b4 = reinterpret_cast<const float4*>(row + head);
+    const Chunk* b = reinterpret_cast<const Chunk*>(row + head);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int q = j * Lanes + t;
-      const float4 v = b4[q < body ? q : body - 1];
-      x[4 * j + 0] = v.x;
-      x[4 * j + 1] = v.y;
-      x[4 * j + 2] = v.z;
-      x[4 * j + 3] = v.w;
+      const Chunk v = b[q < body ? q : body - 1];
+#pragma unroll
+      for (int e = 0; e < kE; ++e) x[kE * j + e] = static_cast<float>(v[e]);
     }
     const int c = extra_col(t, cols);
-    x[4 * V] = row[c >= 0 ? c : 0];
+    x[kE * V] = static_cast<float>(row[c >= 0 ? c : 0]);
   }
 
   __device__ __forceinline__ void mask(int cols, int t, float pad) {
@@ -145,40 +183,45 @@ struct RaggedRowSlice {
     for (int j = 0; j < V; ++j) {
       const bool in = j * Lanes + t < body;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[4 * j + e] = in ? x[4 * j + e] : pad;
+      for (int e = 0; e < kE; ++e) x[kE * j + e] = in ? x[kE * j + e] : pad;
     }
-    x[4 * V] = extra_col(t, cols) >= 0 ? x[4 * V] : pad;
+    x[kE * V] = extra_col(t, cols) >= 0 ? x[kE * V] : pad;
   }
 
-  __device__ __forceinline__ void load(const float* __restrict__ row,
-                                       int cols, int t, float pad) {
+  __device__ __forceinline__ void load(const T* __restrict__ row, int cols,
+                                       int t, float pad) {
     load_raw(row, cols, t);
     mask(cols, t, pad);
   }
 
-  __device__ __forceinline__ void store(float* __restrict__ row, int cols,
+  __device__ __forceinline__ void store(T* __restrict__ row, int cols,
                                         int t) const {
-    float4* b4 = reinterpret_cast<float4*>(row + head);
+    Chunk* b = reinterpret_cast<Chunk*>(row + head);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int q = j * Lanes + t;
-      if (q < body)
-        b4[q] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+      if (q < body) {
+        Chunk v;
+#pragma unroll
+        for (int e = 0; e < kE; ++e) v[e] = static_cast<T>(x[kE * j + e]);
+        b[q] = v;
+      }
     }
     const int c = extra_col(t, cols);
-    if (c >= 0) row[c] = x[4 * V];
+    if (c >= 0) row[c] = static_cast<T>(x[kE * V]);
   }
 };
 
-// Slice type for an access width: 4 -> aligned float4 rows, 1 -> 4-byte
-// elements, 0 -> ragged rows (float4 body at any alignment).
-template <int V, int Lanes, int W>
+// Slice type for an access width: RowElem<T>::kPerChunk -> aligned 16-byte
+// chunks, 1 -> single elements, 0 -> ragged rows (chunk body at any
+// alignment).
+template <int V, int Lanes, int W, typename T = float>
 struct SliceFor {
-  using type = RowSlice<V, Lanes, W>;
+  using type = RowSlice<V, Lanes, W, T>;
 };
-template <int V, int Lanes>
-struct SliceFor<V, Lanes, 0> {
-  using type = RaggedRowSlice<V, Lanes>;
+template <int V, int Lanes, typename T>
+struct SliceFor<V, Lanes, 0, T> {
+  using type = RaggedRowSlice<V, Lanes, T>;
 };
 
 // Same offset modulo 16 bytes.
@@ -190,7 +233,7 @@ enum class RowPath { kWave, kBlock, kTwoPass };
 
 struct RowPlan {
   RowPath path;
-  int vec_width;   // W: 4 or 1
+  int vec_width;   // W: elements per access (1, 4 or 8)
   int per_thread;  // V: accesses per thread (power of two)
 };
 
@@ -200,8 +243,7 @@ inline int next_pow2(int v) {
   return p;
 }
 
-inline RowPlan pick_row_plan(int cols, bool vec4_ok) {
-  const int w = vec4_ok ? 4 : 1;
+inline RowPlan pick_row_plan(int cols, int w) {
   if (cols <= kRowWaveMaxCols)
     return {RowPath::kWave, w, next_pow2((cols + kWaveSize * w - 1) /
                                          (kWaveSize * w))};

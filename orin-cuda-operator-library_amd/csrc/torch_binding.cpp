@@ -65,20 +65,33 @@ at::Tensor reduce_sum_hip(const at::Tensor& input) {
   return output;
 }
 
+// softmax and rmsnorm also take float16 tensors (output float16, fp32
+// arithmetic inside): the reference binding accepts float32 only
+// (operatorlib_binding.cpp:60, :96) and defers FP16 to a later dtype
+// extension (docs/pytorch_extension.md:143-146). Other dtypes still fail
+// with a message naming float32.
 at::Tensor softmax_hip(const at::Tensor& input) {
   check_cuda_contiguous(input, "input");
-  TORCH_CHECK(input.scalar_type() == at::kFloat,
-              "softmax supports float32 input only");
+  const bool half = input.scalar_type() == at::kHalf;
+  TORCH_CHECK(input.scalar_type() == at::kFloat || half,
+              "softmax supports float32 or float16 input only");
   TORCH_CHECK(input.dim() >= 1, "input must have at least one dimension");
   const int cols = checked_positive_int(input.size(-1), "last dimension");
   const int rows =
       checked_positive_int(input.numel() / input.size(-1), "row count");
   const c10::DeviceGuard device_guard(input.device());
   at::Tensor output = at::empty_like(input);
-  check_launch(operatorlib::softmax_f32(input.data_ptr<float>(),
-                                        output.data_ptr<float>(), rows, cols,
-                                        current_stream(input)),
-               "softmax");
+  if (half)
+    check_launch(operatorlib::softmax_f16(
+                     reinterpret_cast<const __half*>(input.data_ptr<at::Half>()),
+                     reinterpret_cast<__half*>(output.data_ptr<at::Half>()),
+                     rows, cols, current_stream(input)),
+                 "softmax");
+  else
+    check_launch(operatorlib::softmax_f32(input.data_ptr<float>(),
+                                          output.data_ptr<float>(), rows, cols,
+                                          current_stream(input)),
+                 "softmax");
   return output;
 }
 
@@ -103,8 +116,9 @@ at::Tensor rmsnorm_hip(const at::Tensor& input, const at::Tensor& weight,
   check_cuda_contiguous(input, "input");
   check_cuda_contiguous(weight, "weight");
   check_same_device_dtype(input, weight, "input", "weight");
-  TORCH_CHECK(input.scalar_type() == at::kFloat,
-              "rmsnorm supports float32 input only");
+  const bool half = input.scalar_type() == at::kHalf;
+  TORCH_CHECK(input.scalar_type() == at::kFloat || half,
+              "rmsnorm supports float32 or float16 input only");
   TORCH_CHECK(input.dim() >= 1, "input must have at least one dimension");
   TORCH_CHECK(weight.dim() == 1, "weight must be 1D");
   TORCH_CHECK(std::isfinite(epsilon) && epsilon > 0.0,
@@ -116,11 +130,20 @@ at::Tensor rmsnorm_hip(const at::Tensor& input, const at::Tensor& weight,
       checked_positive_int(input.numel() / input.size(-1), "token count");
   const c10::DeviceGuard device_guard(input.device());
   at::Tensor output = at::empty_like(input);
-  check_launch(operatorlib::rmsnorm_f32(
-                   input.data_ptr<float>(), weight.data_ptr<float>(),
-                   output.data_ptr<float>(), tokens, hidden,
-                   static_cast<float>(epsilon), current_stream(input)),
-               "rmsnorm");
+  if (half)
+    check_launch(operatorlib::rmsnorm_f16(
+                     reinterpret_cast<const __half*>(input.data_ptr<at::Half>()),
+                     reinterpret_cast<const __half*>(weight.data_ptr<at::Half>()),
+                     reinterpret_cast<__half*>(output.data_ptr<at::Half>()),
+                     tokens, hidden, static_cast<float>(epsilon),
+                     current_stream(input)),
+                 "rmsnorm");
+  else
+    check_launch(operatorlib::rmsnorm_f32(
+                     input.data_ptr<float>(), weight.data_ptr<float>(),
+                     output.data_ptr<float>(), tokens, hidden,
+                     static_cast<float>(epsilon), current_stream(input)),
+                 "rmsnorm");
   return output;
 }
 

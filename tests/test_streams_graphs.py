@@ -48,6 +48,8 @@ def _all_ops(ops, t):
         ops.softmax(t["sm"]),
         ops.transpose(t["tr"]),
         ops.rmsnorm(t["rn"], t["w"], 1e-6),
+        ops.softmax(t["sm"].half()),
+        ops.rmsnorm(t["rn"].half(), t["w"].half(), 1e-6),
         ops.gemm(t["a"], t["b"]),
         ops.gemm(t["ah"], t["bh"]),      # zero-padded workspace path
         ops.gemm(t["a1"], t["b1"]),      # skinny path with K splits
