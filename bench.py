@@ -383,6 +383,25 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         out.append(fl_entry("attention_f16", list(shape), eff, ms_med, ms_mean,
                             FP16_PEAK_TFLOPS, extra))
         del qkv, o
+    # FP32 attention (API coverage; no BASELINE config): the S1024 shape of
+    # the FP16 configs, and a shape with enough workgroups to fill the GPU.
+    for bsz, heads, seq, causal in [(1, 12, 1024, False), (4, 32, 2048, False),
+                                    (4, 32, 2048, True)]:
+        if not want("attention") and not want("attention_f32"):
+            break
+        d = 128
+        shape = (bsz, heads, seq, d)
+        gen = torch.Generator(device=dev).manual_seed(31)
+        qkv = [torch.randn(shape, device=dev, generator=gen) for _ in range(3)]
+        o = torch.empty(shape, device=dev)
+        f = lambda i: lib.operatorlib_attention_f32(ptr(qkv[0]), ptr(qkv[1]), ptr(qkv[2]), ptr(o),
+                                                    bsz, heads, seq, d, int(causal), stream)
+        dense = 4 * bsz * heads * seq * seq * d
+        eff = 4 * bsz * heads * d * seq * (seq + 1) // 2 if causal else dense
+        ms_med, ms_mean = time_single(torch, f, max(5, min(steps, 20)), 3)
+        out.append(fl_entry("attention_f32", list(shape), eff, ms_med, ms_mean,
+                            FP32_PEAK_TFLOPS, {"causal": causal}))
+        del qkv, o
     torch.cuda.empty_cache()
     return out
 
