@@ -4,9 +4,9 @@
 //
 // Cross-lane reductions use the CDNA data-parallel primitives instead of
 // generic shuffles: DPP quad permutes and row mirrors combine lanes inside a
-// 16-lane row, ds_swizzle (bit-mask mode) combines the two rows of each
-// 32-lane half, and two v_readlane_b32 combine the halves into a wave-uniform
-// scalar. Every step is a full butterfly, so all lanes see identical bits and
+// 16-lane row, v_permlane16_swap (gfx950, register to register) combines the
+// two rows of each 32-lane half, and two v_readlane_b32 combine the halves
+// into a wave-uniform scalar. Every step is a full butterfly, so all lanes see identical bits and
 // the result is independent of scheduling (bitwise deterministic).
 //
 // The reductions require all 64 lanes to be active: callers pad inactive
@@ -26,8 +26,6 @@ constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
 constexpr int kDppRowMirror = 0x140;     // lane i <-> 15-i within 16 lanes
-// ds_swizzle bit-mask mode: and=0x1f, or=0, xor=0x10 -> lane ^ 16.
-constexpr int kSwizzleXor16 = 0x401F;
 
 template <int Ctrl>
 __device__ __forceinline__ int dpp_i32(int v) {
@@ -51,23 +49,31 @@ __device__ __forceinline__ double dpp_f64(double v) {
   return __builtin_bit_cast(double, out);
 }
 
-__device__ __forceinline__ float swizzle_xor16_f32(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v),
-                                         kSwizzleXor16));
+// The value of lane l ^ 16 as the pair (own row's value, partner row's
+// value) in both lanes: v_permlane16_swap with both operands v returns
+// rows (0, 0, 2, 2) and (1, 1, 3, 3) of v. Op::apply on the pair gives
+// the lane ^ 16 combination with the lower row's value first in every lane.
+template <class Op>
+__device__ __forceinline__ float combine_xor16_f32(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return Op::apply(__builtin_bit_cast(float, static_cast<unsigned>(r[0])),
+                   __builtin_bit_cast(float, static_cast<unsigned>(r[1])));
 }
 
-__device__ __forceinline__ double swizzle_xor16_f64(double v) {
+__device__ __forceinline__ double sum_xor16_f64(double v) {
   const std::uint64_t bits = __builtin_bit_cast(std::uint64_t, v);
-  const int lo = __builtin_amdgcn_ds_swizzle(
-      static_cast<int>(bits & 0xffffffffu), kSwizzleXor16);
-  const int hi =
-      __builtin_amdgcn_ds_swizzle(static_cast<int>(bits >> 32), kSwizzleXor16);
-  const std::uint64_t out = (static_cast<std::uint64_t>(
-                                 static_cast<std::uint32_t>(hi))
-                             << 32) |
-                            static_cast<std::uint32_t>(lo);
-  return __builtin_bit_cast(double, out);
+  const unsigned lo = static_cast<unsigned>(bits & 0xffffffffu);
+  const unsigned hi = static_cast<unsigned>(bits >> 32);
+  const auto rl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto rh = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  const double a = __builtin_bit_cast(
+      double, (static_cast<std::uint64_t>(static_cast<unsigned>(rh[0])) << 32) |
+                  static_cast<unsigned>(rl[0]));
+  const double b = __builtin_bit_cast(
+      double, (static_cast<std::uint64_t>(static_cast<unsigned>(rh[1])) << 32) |
+                  static_cast<unsigned>(rl[1]));
+  return a + b;
 }
 
 __device__ __forceinline__ float readlane_f32(float v, int lane) {
@@ -105,7 +111,7 @@ __device__ __forceinline__ float wave_reduce(float v) {
   v = Op::apply(v, dpp_f32<kDppQuadXor2>(v));
   v = Op::apply(v, dpp_f32<kDppRowHalfMirror>(v));
   v = Op::apply(v, dpp_f32<kDppRowMirror>(v));
-  v = Op::apply(v, swizzle_xor16_f32(v));
+  v = combine_xor16_f32<Op>(v);
   return Op::apply(readlane_f32(v, 0), readlane_f32(v, 32));
 }
 
@@ -114,7 +120,7 @@ __device__ __forceinline__ double wave_reduce_sum_f64(double v) {
   v += dpp_f64<kDppQuadXor2>(v);
   v += dpp_f64<kDppRowHalfMirror>(v);
   v += dpp_f64<kDppRowMirror>(v);
-  v += swizzle_xor16_f64(v);
+  v = sum_xor16_f64(v);
   return readlane_f64(v, 0) + readlane_f64(v, 32);
 }
 
