@@ -727,14 +727,29 @@ void skinny_kernel(
   }
 }
 
-// out[i] = sum over splits s (in order) of part[s][i].
-__global__ __launch_bounds__(256) void sum_splits_kernel(
+// out[i] = sum over splits s (in order) of part[s][i]. Each thread issues
+// the loads of up to kSplitBatch splits before adding them, so a sum costs
+// one memory round trip per batch instead of one per split.
+constexpr int kSplitBatch = 16;
+constexpr int kSumThreads = 64;
+
+__global__ __launch_bounds__(kSumThreads) void sum_splits_kernel(
     const float* __restrict__ part, float* __restrict__ out, long long count,
     int splits) {
-  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < count;
-       i += static_cast<long long>(gridDim.x) * 256) {
+  for (long long i = blockIdx.x * static_cast<long long>(kSumThreads) + threadIdx.x;
+       i < count; i += static_cast<long long>(gridDim.x) * kSumThreads) {
     float s = part[i];
-    for (int p = 1; p < splits; ++p) s += part[p * count + i];
+    for (int p0 = 1; p0 < splits; p0 += kSplitBatch) {
+      float v[kSplitBatch];
+#pragma unroll
+      for (int u = 0; u < kSplitBatch; ++u) {
+        const int p = min(p0 + u, splits - 1);  // in range; extra slots unused
+        v[u] = part[p * count + i];
+      }
+#pragma unroll
+      for (int u = 0; u < kSplitBatch; ++u)
+        if (p0 + u < splits) s += v[u];
+    }
     out[i] = s;
   }
 }
@@ -781,9 +796,9 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k,
   else launch_m<T, 16>(a, b, dst, m, n, k, chunk, grid, stream);
   if (splits > 1) {
     const long long count = static_cast<long long>(m) * n;
-    const long long blocks = (count + 255) / 256;
-    sum_splits_kernel<<<dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
-                        dim3(256), 0, stream>>>(dst, c, count, splits);
+    const long long blocks = (count + kSumThreads - 1) / kSumThreads;
+    sum_splits_kernel<<<dim3(static_cast<unsigned>(blocks < 16384 ? blocks : 16384)),
+                        dim3(kSumThreads), 0, stream>>>(dst, c, count, splits);
   }
   return hipGetLastError();
 }
