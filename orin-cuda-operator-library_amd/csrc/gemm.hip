@@ -528,10 +528,13 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
 //     a fixed order;
 //   * K is split over enough workgroups to fill the GPU; per-split partials
 //     go to the stream's workspace and a second kernel sums them in split
-//     order, so results are deterministic.
+//     order, so results are deterministic;
+//   * from M = 5 (fp16) or 9 (fp32) the vector-ALU dot products cost more
+//     than the B stream, and skinny_mfma_kernel (below) takes over.
 namespace skinny {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4v __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kMaxM = 16;
@@ -545,6 +548,10 @@ struct Cfg {
   static constexpr int kPerLane = 16 / sizeof(T);       // columns per lane
   static constexpr int kBlockN = kLanesPerRow * kPerLane;  // 64 fp32, 128 fp16
   static constexpr int kRowsPerStep = sizeof(T) == 2 ? 2 : 1;  // dot2 pairs
+  // From this M on the matrix-core variant is faster (measured on MI355X,
+  // N = K = 4096: fp16 M 4 -> 11.3 us vector ALU, M 6 -> 12.3 us matrix
+  // cores; fp32 M 8 -> 18.7 / 20.6 us, M 12 -> 27.9 / 21.9 us).
+  static constexpr int kMfmaMinM = sizeof(T) == 2 ? 5 : 9;
 };
 
 // Row steps (16-byte loads of one or two rows) in flight per thread per
@@ -727,6 +734,145 @@ void skinny_kernel(
   }
 }
 
+// Matrix-core variant for larger M (up to 16): one v_mfma_f32_16x16x16_f16
+// (fp16) or v_mfma_f32_16x16x4_f32 (fp32) turns 16 rows of A times a 16 x 16
+// block of B into a 16 x 16 block of C, where the vector-ALU kernel spends
+// one dot product per (m, column pair) and becomes ALU-bound as M grows.
+// B is never transposed: the MFMA only needs A and B to agree on which k
+// fills each of its k slots, so lane (g, c) (g = lane / 16, c = lane % 16)
+// loads 16-byte chunks of its R rows (k slots R*g .. R*g+R-1) at columns
+// P*c .. P*c+P-1, and MFMA j takes column j of every lane's chunk: tile
+// column c of MFMA j is matrix column P*c + j, so P MFMAs cover the
+// workgroup's 16 P columns. Each lane reads its A operand values straight
+// from global memory (L2-resident) with its B loads, so nothing waits on a
+// staging barrier. Splits, the workgroup shape and the partial sums are
+// those of skinny_kernel.
+template <typename T>
+struct MfmaCfg;
+template <>
+struct MfmaCfg<_Float16> {
+  typedef _Float16 AOp __attribute__((ext_vector_type(4)));
+  static constexpr int kRows = 4;     // B rows per lane per k block
+  static constexpr int kK = 16;       // k per MFMA = rows per k block
+  static constexpr int kBatch = 4;    // k blocks in flight per wavefront
+  __device__ static floatx4v mma(AOp a, AOp b, floatx4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct MfmaCfg<float> {
+  typedef float AOp;
+  static constexpr int kRows = 1;
+  static constexpr int kK = 4;
+  static constexpr int kBatch = 16;
+  __device__ static floatx4v mma(AOp a, AOp b, floatx4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
+    const T* __restrict__ A, const T* __restrict__ B, float* __restrict__ out,
+    int m_rows, int n, int k, int chunk) {
+  using MC = MfmaCfg<T>;
+  using Vec = typename RowChunk<T>::Vec;  // one 16-byte chunk of a B row
+  using AOp = typename MC::AOp;
+  constexpr int P = Cfg<T>::kPerLane;     // columns per lane
+  constexpr int BN = Cfg<T>::kBlockN;     // 16 * P
+  constexpr int R = MC::kRows;
+  constexpr int KB = MC::kK;
+  constexpr int kBatch = MC::kBatch;
+  __shared__ float red[kWaves * opl::kWaveSize * P * 4];
+
+  const int n0 = blockIdx.x * BN;
+  const int k0 = blockIdx.y * chunk;
+  const int k_end = min(k, k0 + chunk);
+  const int tid = threadIdx.x;
+  const int lane = tid % opl::kWaveSize;
+  const int wave = tid / opl::kWaveSize;
+  const int g = lane / 16;
+  const int c = lane % 16;
+  // Columns past N: read a valid chunk (n % P == 0), results not stored.
+  const int col = min(n0 + c * P, n - P);
+  const bool a_row = c < m_rows;  // A row c of the MFMA A operand exists
+  const int blocks = (k_end - k0 + KB - 1) / KB;
+
+  // k block b, lane group g: k rows k0 + KB b + R g + q (q < R). B: a
+  // 16-byte chunk of each row; A operand: A[c][row] (read from L2, every
+  // workgroup of the split reads the same A). Rows past k_end read valid
+  // memory and are zeroed, as are A rows past m_rows.
+  auto load_block = [&](int b, Vec (&v)[R], AOp& a) {
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const int r = k0 + KB * b + R * g + q;
+      const bool in = r < k_end;
+      const int rc = in ? r : k_end - 1;
+      Vec x = *reinterpret_cast<const Vec*>(B + static_cast<std::size_t>(rc) * n + col);
+#pragma unroll
+      for (int j = 0; j < P; ++j) x[j] = in ? x[j] : T(0);
+      v[q] = x;
+      const bool a_in = in && a_row;
+      const T av = A[a_in ? static_cast<std::size_t>(c) * k + r : 0];
+      if constexpr (R == 1)
+        a = a_in ? av : T(0);
+      else
+        a[q] = a_in ? av : T(0);
+    }
+  };
+
+  floatx4v acc[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[j][e] = 0.0f;
+
+  Vec v[kBatch][R];
+  AOp a[kBatch];
+  for (int b0 = wave; b0 < blocks; b0 += kWaves * kBatch) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int b = b0 + kWaves * u;
+      load_block(b < blocks ? b : blocks - 1, v[u], a[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (b0 + kWaves * u < blocks) {  // wave-uniform
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+          AOp bop;
+          if constexpr (R == 4) {
+#pragma unroll
+            for (int q = 0; q < R; ++q) bop[q] = v[u][q][j];
+          } else {
+            bop = v[u][0][j];
+          }
+          acc[j] = MC::mma(a[u], bop, acc[j]);
+        }
+      }
+    }
+  }
+
+  // acc[j][i] = C[4 g + i][n0 + P c + j] of this wavefront's k blocks.
+#pragma unroll
+  for (int j = 0; j < P; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      red[((wave * opl::kWaveSize + lane) * P + j) * 4 + i] = acc[j][i];
+  __syncthreads();
+  float* dst = out + static_cast<std::size_t>(blockIdx.y) * m_rows * n;
+  for (int o = tid; o < 16 * BN; o += kThreads) {
+    const int m = o / BN;
+    const int co = o % BN;
+    if (m < m_rows && n0 + co < n) {
+      const int src = ((16 * (m / 4) + co / P) * P + co % P) * 4 + m % 4;
+      float s = red[src];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) s += red[w * opl::kWaveSize * P * 4 + src];
+      dst[static_cast<std::size_t>(m) * n + n0 + co] = s;
+    }
+  }
+}
+
 // out[i] = sum over splits s (in order) of part[s][i]. Each thread issues
 // the loads of up to kSplitBatch splits before adding them, so a sum costs
 // one memory round trip per batch instead of one per split.
@@ -789,7 +935,9 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k,
     dst = static_cast<float*>(ws);
   }
   const dim3 grid(static_cast<unsigned>(blocks_n), static_cast<unsigned>(splits));
-  if (m == 1) launch_m<T, 1>(a, b, dst, m, n, k, chunk, grid, stream);
+  if (m >= C::kMfmaMinM)
+    skinny_mfma_kernel<T><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k, chunk);
+  else if (m == 1) launch_m<T, 1>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 2) launch_m<T, 2>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 4) launch_m<T, 4>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 8) launch_m<T, 8>(a, b, dst, m, n, k, chunk, grid, stream);

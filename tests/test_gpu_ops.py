@@ -248,7 +248,10 @@ def test_gemm_f16_small(hip, mnk, offset):
 # M <= 16 (decode shapes): the skinny kernels, with and without K splits,
 # partial column blocks and odd K.
 GEMM_SKINNY = [(1, 4096, 4096), (4, 4096, 4096), (16, 4096, 4096), (3, 1000, 333),
-               (16, 4104, 1000), (1, 8, 5000), (9, 136, 777), (2, 64, 31), (1, 1024, 1)]
+               (16, 4104, 1000), (1, 8, 5000), (9, 136, 777), (2, 64, 31), (1, 1024, 1),
+               # matrix-core variant (M >= 5 fp16, >= 9 fp32): K tails inside
+               # a k block, a partial column block, one split
+               (5, 264, 1001), (12, 72, 37), (8, 4096, 4096), (13, 520, 4099)]
 
 
 @pytest.mark.parametrize("mnk", GEMM_SKINNY)
@@ -275,6 +278,12 @@ def test_gemm_skinny_deterministic(hip):
     first = hip.gemm_f32(a, b)
     for _ in range(3):
         assert np.array_equal(hip.gemm_f32(a, b), first)
+    # matrix-core variant (fp16, M >= 5)
+    ah = oracle.to_f16_bits(oracle.uniform(652, (12, 4096)))
+    bh = oracle.to_f16_bits(oracle.uniform(653, (4096, 2048)))
+    first = hip.gemm_f16(ah, bh)
+    for _ in range(3):
+        assert np.array_equal(hip.gemm_f16(ah, bh), first)
 
 
 # Large shapes that miss the fast kernels' rules and run on zero-padded
