@@ -67,7 +67,7 @@ __global__ __launch_bounds__(opl::kRowWaveThreads) void softmax_wave_kernel(
   if (row >= rows) return;  // uniform per wavefront
   const std::size_t offset = static_cast<std::size_t>(row) * cols;
   typename opl::SliceFor<V, opl::kWaveSize, W, T>::type s;
-  s.load(input + offset, cols, lane, -INFINITY);
+  s.template load<true>(input + offset, cols, lane, -INFINITY);
   const float m = opl::wave_reduce<opl::MaxOp>(local_max(s.x));
   const float sum = opl::wave_reduce<opl::SumOp>(exp_shift_sum(s.x, m));
   scale(s.x, 1.0f / sum);
@@ -81,7 +81,7 @@ __global__ __launch_bounds__(opl::kRowBlockThreads) void softmax_block_kernel(
   __shared__ float sum_slots[opl::kRowBlockWaves];
   const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
   typename opl::SliceFor<V, opl::kRowBlockThreads, W, T>::type s;
-  s.load(input + offset, cols, threadIdx.x, -INFINITY);
+  s.template load<true>(input + offset, cols, threadIdx.x, -INFINITY);
   const float m = opl::block_reduce<opl::MaxOp, opl::kRowBlockWaves>(
       local_max(s.x), max_slots);
   const float sum = opl::block_reduce<opl::SumOp, opl::kRowBlockWaves>(
