@@ -55,7 +55,7 @@ __global__ __launch_bounds__(opl::kRowWaveThreads) void rmsnorm_wave_kernel(
   if (row >= rows) return;  // uniform per wavefront
   const std::size_t offset = static_cast<std::size_t>(row) * cols;
   opl::RowSlice<V, opl::kWaveSize, W, T> s;
-  s.load(input + offset, cols, lane, 0.0f);
+  s.template load<true>(input + offset, cols, lane, 0.0f);
   const float ss = opl::wave_reduce<opl::SumOp>(sum_squares(s.x));
   const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
   scale_store(s, weight, output + offset, cols, lane, inv);
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(opl::kRowBlockThreads) void rmsnorm_block_kernel(
   __shared__ float slots[opl::kRowBlockWaves];
   const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
   opl::RowSlice<V, opl::kRowBlockThreads, W, T> s;
-  s.load(input + offset, cols, threadIdx.x, 0.0f);
+  s.template load<true>(input + offset, cols, threadIdx.x, 0.0f);
   const float ss = opl::block_reduce<opl::SumOp, opl::kRowBlockWaves>(
       sum_squares(s.x), slots);
   const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(opl::kRowWaveThreads) void rmsnorm_ragged_wave_kern
     wv[i] = weight[c < cols ? c : cols - 1];
   }
   opl::RaggedRowSlice<V, opl::kWaveSize, T> s;
-  s.load_raw(input + offset, cols, lane);  // row 0 stands in for inactive waves
+  s.template load_raw<true>(input + offset, cols, lane);  // row 0 stands in for inactive waves
   __builtin_amdgcn_sched_barrier(0);       // keep the row's loads in flight
   // Every slot written (those at or past `cols` repeat the last weight and
   // are never read), so the writes need no branches.
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(opl::kRowBlockThreads) void rmsnorm_ragged_block_ke
   __shared__ float slots[opl::kRowBlockWaves];
   const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
   opl::RaggedRowSlice<V, opl::kRowBlockThreads, T> s;
-  s.load(input + offset, cols, threadIdx.x, 0.0f);
+  s.template load<true>(input + offset, cols, threadIdx.x, 0.0f);
   const float ss = opl::block_reduce<opl::SumOp, opl::kRowBlockWaves>(
       sum_squares(s.x), slots);
   const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
