@@ -953,9 +953,38 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k,
 
 }  // namespace skinny
 
+typedef unsigned uint4v __attribute__((ext_vector_type(4)));
+
+// The 16 bytes at p (any 2-byte alignment) from the aligned 16-byte
+// chunk(s) covering them: word i of the result is bytes sh + 4i .. sh + 4i
+// + 3 of the two chunks, sh = p mod 16, taken with v_alignbyte. Both chunks
+// hold bytes of [p, p + 16), so they lie in pages those bytes occupy.
+__device__ __forceinline__ uint4v load16_shifted(const void* p) {
+  const std::uintptr_t addr = reinterpret_cast<std::uintptr_t>(p);
+  const int sh = static_cast<int>(addr & 15);
+  const uint4v* a = reinterpret_cast<const uint4v*>(addr - sh);
+  const uint4v lo = a[0];
+  if (sh == 0) return lo;
+  const uint4v hi = a[1];
+  const unsigned bs = static_cast<unsigned>(sh & 3);
+  auto ab = [&](unsigned h, unsigned l) { return __builtin_amdgcn_alignbyte(h, l, bs); };
+  uint4v out;
+  switch (sh >> 2) {  // first source word; uniform across a row's chunks
+    case 0: out = uint4v{ab(lo[1], lo[0]), ab(lo[2], lo[1]), ab(lo[3], lo[2]), ab(hi[0], lo[3])}; break;
+    case 1: out = uint4v{ab(lo[2], lo[1]), ab(lo[3], lo[2]), ab(hi[0], lo[3]), ab(hi[1], hi[0])}; break;
+    case 2: out = uint4v{ab(lo[3], lo[2]), ab(hi[0], lo[3]), ab(hi[1], hi[0]), ab(hi[2], hi[1])}; break;
+    default: out = uint4v{ab(hi[0], lo[3]), ab(hi[1], hi[0]), ab(hi[2], hi[1]), ab(hi[3], hi[2])}; break;
+  }
+  return out;
+}
+
 // Copies a row-major [rows, cols] matrix into a zero-padded row-major
 // [rows_p, cols_p] one (cols_p a multiple of one 16-byte chunk, 16-byte
-// aligned destination): each thread writes whole chunks.
+// aligned destination): each thread writes whole chunks. A chunk whose
+// source elements all exist is read as 16 bytes from the aligned chunk(s)
+// covering it (rows of an odd-width fp16 matrix start at any 2-byte
+// phase); the last chunk of a row and the padding rows go element by
+// element.
 template <typename T>
 __global__ __launch_bounds__(256) void pad_copy_kernel(
     const T* __restrict__ src, int rows, int cols, T* __restrict__ dst,
@@ -970,9 +999,13 @@ __global__ __launch_bounds__(256) void pad_copy_kernel(
     const int c0 = static_cast<int>(i % per_row) * E;
     const T* s = src + static_cast<std::size_t>(r) * cols;
     Chunk v;
+    if (r < rows && c0 + E <= cols) {
+      v = __builtin_bit_cast(Chunk, load16_shifted(s + c0));
+    } else {
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-      v[e] = (r < rows && c0 + e < cols) ? s[c0 + e] : T(0);
+      for (int e = 0; e < E; ++e)
+        v[e] = (r < rows && c0 + e < cols) ? s[c0 + e] : T(0);
+    }
     *reinterpret_cast<Chunk*>(dst + static_cast<std::size_t>(r) * cols_p + c0) = v;
   }
 }
