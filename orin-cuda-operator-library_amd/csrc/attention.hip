@@ -426,11 +426,12 @@ void launch_attention(const T* q, const T* k, const T* v, float* out, int bh,
 
 // ---------------------------------------------------------------------------
 // attention_f16_dma_kernel — fp16 fast path (head_dim 64 or 128, S % 128 == 0,
-// 16-byte aligned tensors). Same maths, lane layout and accumulation order as
-// attention_mfma_kernel (results are bitwise identical); what changes is how
-// K and V reach the matrix cores:
-//   * K / V tiles are copied global -> LDS with global_load_lds_dwordx4 (no
-//     VGPR staging, no ds_write, no register transpose of V);
+// 16-byte aligned tensors). Same maths and lane layout as
+// attention_mfma_kernel; its running max moves lazily (below), so results
+// agree up to rounding. What changes is how K and V reach the matrix cores:
+//   * K / V tiles are copied global -> LDS by buffer loads with the lds
+//     modifier (buffer_load_dwordx4 ... lds: no VGPR staging, no ds_write,
+//     no register transpose of V); the tile's position is a scalar offset;
 //   * V stays [key][d] in LDS; its V^T MFMA operand is read with
 //     ds_read_b64_tr_b16 (within each 16-lane group, lane 4r + j addresses 4
 //     dims of key row r, lane i receives dim i of rows r = 0..3), which also

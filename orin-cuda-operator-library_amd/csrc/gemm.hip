@@ -291,9 +291,10 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 //     (N), each owning 128 x 64 = 4 x 2 MFMA 32x32x16 blocks (128 fp32
 //     accumulators, so two wavefronts fit per SIMD and one's LDS waits are
 //     covered by the other's MFMAs);
-//   * A and B are copied global -> LDS by global_load_lds_dwordx4 (each lane
-//     writes 16 bytes at LDS base + 16 * lane), so operands never pass
-//     through VGPRs and no ds_write is issued;
+//   * A and B are copied global -> LDS by buffer loads with the lds
+//     modifier (each lane writes 16 bytes at LDS base + 16 * lane) from
+//     per-step scalar bases, so operands never pass through VGPRs and no
+//     ds_write is issued;
 //   * both tiles keep their global layout (A [m][k], B [k][n]); B fragments
 //     are read with ds_read_b64_tr_b16, which returns k-contiguous fp16
 //     pairs from n-contiguous rows: within each 16-lane group, lane 4r + j
@@ -309,8 +310,8 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 //     matrix cores (sched_barrier keeps that order);
 //   * M / N edges: source rows / columns are clamped into the matrix (their
 //     results are never stored), stores are masked.
-// Measured on MI355X (8192^3): ~1.09 PFLOP/s, about 90% of hipBLASLt's
-// fp16 GEMM on the same box.
+// Measured on MI355X (8192^3): 1.01-1.07 PFLOP/s, 84-88% of hipBLASLt's
+// fp16 GEMM on the same box (1.21 PFLOP/s).
 // ---------------------------------------------------------------------------
 
 namespace dma {
