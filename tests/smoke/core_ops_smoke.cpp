@@ -1,4 +1,5 @@
-// core_ops_smoke: reduce, softmax, transpose and RMSNorm through the C++ API.
+// core_ops_smoke: reduce, softmax, transpose and RMSNorm through the C++ API
+// (plus the FP16 softmax / RMSNorm launchers this library adds).
 //
 // Same cases as the reference's tests/core_ops_smoke.cu:165-180 (iota
 // reduce, softmax 19x128 / 17x1024 at range 5 and 17x1003 at range 1000,
@@ -96,6 +97,54 @@ void rmsnorm_case(hipStream_t stream, int tokens, int hidden) {
   smoke::report(name, worst <= 1e-5, worst, 1e-5);
 }
 
+// FP16 rows (softmax_f16 / rmsnorm_f16, not in the reference API): fp16 in
+// and out, fp32 arithmetic; each output within one fp16 ulp of the fp64
+// oracle on the same fp16 inputs (|y - ref| <= 2^-10 |ref| + 2^-24).
+double f16_error(const std::vector<__half>& got, const std::vector<double>& want) {
+  std::vector<std::uint16_t> bits(got.size());
+  std::memcpy(bits.data(), got.data(), bits.size() * sizeof(std::uint16_t));
+  std::vector<float> y(got.size());
+  oracle_f16_to_f32_array(bits.data(), y.data(), y.size());
+  double worst = 0.0;  // in units of the bound
+  for (std::size_t i = 0; i < y.size(); ++i) {
+    if (!std::isfinite(y[i])) return INFINITY;
+    const double bound = std::ldexp(std::abs(want[i]), -10) + std::ldexp(1.0, -24);
+    worst = std::max(worst, std::abs(y[i] - want[i]) / bound);
+  }
+  return worst;
+}
+
+void softmax_f16_case(hipStream_t stream, int rows, int cols, float range) {
+  const std::size_t count = static_cast<std::size_t>(rows) * cols;
+  std::vector<float> x = smoke::uniform(21 + rows + cols, count, -range, range);
+  const std::vector<__half> hx = smoke::to_half(x);  // x now holds the fp16 values
+  smoke::DeviceArray<__half> in(hx, stream), out(count);
+  SMOKE_HIP(operatorlib::softmax_f16(in.get(), out.get(), rows, cols, stream));
+  std::vector<double> want(count);
+  oracle_softmax(x.data(), want.data(), rows, cols);
+  const double worst = f16_error(out.download(stream), want);
+  char name[64];
+  std::snprintf(name, sizeof name, "softmax_f16[%dx%d,range%g]", rows, cols, range);
+  smoke::report(name, worst <= 1.0, worst, 1.0);
+}
+
+void rmsnorm_f16_case(hipStream_t stream, int tokens, int hidden) {
+  constexpr float eps = 1.0e-5f;
+  const std::size_t count = static_cast<std::size_t>(tokens) * hidden;
+  std::vector<float> x = smoke::uniform(31 + tokens, count, -3.0f, 3.0f);
+  std::vector<float> w = smoke::uniform(32 + hidden, hidden, 0.5f, 1.5f);
+  const std::vector<__half> hx = smoke::to_half(x), hw = smoke::to_half(w);
+  smoke::DeviceArray<__half> in(hx, stream), weight(hw, stream), out(count);
+  SMOKE_HIP(operatorlib::rmsnorm_f16(in.get(), weight.get(), out.get(), tokens,
+                                     hidden, eps, stream));
+  std::vector<double> want(count);
+  oracle_rmsnorm(x.data(), w.data(), want.data(), tokens, hidden, eps);
+  const double worst = f16_error(out.download(stream), want);
+  char name[64];
+  std::snprintf(name, sizeof name, "rmsnorm_f16[%dx%d]", tokens, hidden);
+  smoke::report(name, worst <= 1.0, worst, 1.0);
+}
+
 void rejects_invalid_arguments(hipStream_t stream) {
   float* p = reinterpret_cast<float*>(0x1000);  // never dereferenced
   const bool ok =
@@ -119,6 +168,10 @@ int main() {
   transpose_iota(stream);
   rmsnorm_case(stream, 32, 4096);
   rmsnorm_case(stream, 17, 1003);
+  softmax_f16_case(stream, 19, 128, 5.0f);
+  softmax_f16_case(stream, 17, 1003, 5.0f);
+  rmsnorm_f16_case(stream, 32, 4096);
+  rmsnorm_f16_case(stream, 17, 1003);
   rejects_invalid_arguments(stream);
   SMOKE_HIP(hipStreamDestroy(stream));
   return smoke::finish("core_ops_smoke");
