@@ -538,15 +538,19 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     k_src[j] *= 2;  // elements -> bytes
     v_src[j] *= 2;
   }
+  // The copies' LDS destinations (M0) are wave-uniform: derived from a
+  // scalar copy of the wave index, they stay in scalar registers instead of
+  // costing a v_readfirstlane per copy and tile.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto issue = [&](unsigned char* st, int key0) {
     const int tile_bytes = key0 * D * 2;
 #pragma unroll
     for (int j = 0; j < L::kCopies; ++j)
-      opl::buffer_copy16_lds(kh, head_bytes, st + (wave * L::kCopies + j) * 1024,
+      opl::buffer_copy16_lds(kh, head_bytes, st + (wave_s * L::kCopies + j) * 1024,
                         k_src[j], tile_bytes);
 #pragma unroll
     for (int j = 0; j < L::kCopies; ++j)
-      opl::buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave * L::kCopies + j) * 1024,
+      opl::buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave_s * L::kCopies + j) * 1024,
                         v_src[j], tile_bytes);
   };
   // K^T-operand rows are l32 (+32 for the second 32-key block, an immediate).
@@ -574,6 +578,10 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
   float row_max = -FLT_MAX;
   float row_sum = 0.0f;
+  // Raw score above which the running max must move; -inf until the first
+  // visible score.
+  float move_above = -INFINITY;
+  const float inv_scale = 1.0f / score_scale_log2;
   const int visible_end = causal ? min(S, q0 + kBlockRows) : S;
   const int tiles = (visible_end + kKeys - 1) / kKeys;
 
@@ -607,25 +615,28 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
           if (key > my_row) s[e] = -INFINITY;
         }
       };
-      // Row max of a half (log2 units), both lane halves combined.
-      auto scaled_max = [&](const floatx16& s) {
+      // Row max of a half's raw scores, both lane halves combined
+      // (v_maximum3_f32: 8 instructions for 16 values).
+      auto half_max = [&](const floatx16& s) {
         float m = s[0];
 #pragma unroll
-        for (int e = 1; e < 16; ++e) m = fmaxf(m, s[e]);
-        return opl::max_lane_xor32(m) * score_scale_log2;
+        for (int e = 1; e < 16; ++e) m = __builtin_elementwise_maximum(m, s[e]);
+        return opl::max_lane_xor32(m);
       };
       // Lazy rescaling: the running max m (log2 units) only moves when a
       // row's max exceeds it by more than kLazyLog2, so p = 2^(x - m) stays
       // <= 2^kLazyLog2 (well inside fp16's range) and the O rescale is
       // skipped on almost every half-tile. Softmax is shift-invariant: the
-      // result is the same up to rounding.
-      auto needs_move = [&](float cand) {
-        return __builtin_amdgcn_ballot_w64(cand > row_max + kLazyLog2) != 0;
+      // result is the same up to rounding. The test compares raw scores
+      // with move_above = (m + kLazyLog2) / scale, updated when m moves.
+      auto needs_move = [&](float raw) {
+        return __builtin_amdgcn_ballot_w64(raw > move_above) != 0;
       };
-      auto move_max = [&](float cand) {
-        const float new_max = fmaxf(row_max, cand);
+      auto move_max = [&](float raw) {
+        const float new_max = fmaxf(row_max, raw * score_scale_log2);
         const float alpha = opl::fast_exp2(row_max - new_max);
         row_max = new_max;
+        move_above = (new_max + kLazyLog2) * inv_scale;
         row_sum *= alpha;
 #pragma unroll
         for (int dt = 0; dt < L::kDTiles; ++dt)
@@ -667,13 +678,13 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
         half8 p0[2], p1[2];
         floatx16 s0 = scores(0);
         if constexpr (kMasked) mask(s0, 0);
-        const float c0 = scaled_max(s0);
+        const float c0 = half_max(s0);
         if (needs_move(c0)) move_max(c0);
         floatx16 s1 = scores(1);
         row_sum += exponentiate(s0, p0);
         accumulate(0, p0);
         if constexpr (kMasked) mask(s1, 1);
-        const float c1 = scaled_max(s1);
+        const float c1 = half_max(s1);
         float ps1 = exponentiate(s1, p1);
         if (needs_move(c1)) {
           move_max(c1);  // after P.V of half 0, which used the old max

@@ -179,11 +179,13 @@ __device__ __forceinline__ void buffer_copy16_lds(const void* base, unsigned byt
 // max / sum of v over lanes l and l ^ 32 (the two halves of a wavefront),
 // the same value in both lanes. v_permlane32_swap exchanges the halves
 // register to register, where __shfl_xor(v, 32) is an LDS round trip
-// (ds_bpermute). Sums add the lower half's value first in every lane.
+// (ds_bpermute). Sums add the lower half's value first in every lane. The
+// max is IEEE maximum (NaN-propagating, v_maximum_f32), which needs none
+// of the canonicalising moves fmaxf adds.
 __device__ __forceinline__ float max_lane_xor32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
                                                   __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float sum_lane_xor32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
