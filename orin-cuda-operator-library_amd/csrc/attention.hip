@@ -600,12 +600,18 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
         floatx16 s;
 #pragma unroll
         for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+        half8 a[L::kSteps];
 #pragma unroll
-        for (int c = 0; c < L::kSteps; ++c) {
-          const half8 a = *reinterpret_cast<const half8*>(
+        for (int c = 0; c < L::kSteps; ++c)
+          a[c] = *reinterpret_cast<const half8*>(
               cur + k_off[c] + kb * 32 * L::kRowBytes);
-          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
-        }
+        // All K reads of the half are issued before the MFMA chain: with
+        // one workgroup per CU (small grids) nothing else hides their
+        // latency (B1 H12 S1024: 22.8 -> 22.3 us).
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < L::kSteps; ++c)
+          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[c], s, 0, 0, 0);
         return s;
       };
       auto mask = [&](floatx16& s, int kb) {
