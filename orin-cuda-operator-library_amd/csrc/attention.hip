@@ -440,10 +440,12 @@ void launch_attention(const T* q, const T* k, const T* v, float* out, int bh,
 //     use chunk ^ (row & 15) (D = 128) or ^ ((row >> 1) & 7) (D = 64), V rows
 //     chunk ^ 4 * (row & 3) / ^ 4 * ((row >> 1) & 1); the swizzle terms are
 //     lane constants, so per-tile offsets fold into instruction immediates;
-//   * ~250 VGPRs and 64 KiB of LDS, so two 4-wavefront workgroups share a CU:
-//     one wavefront's softmax VALU work overlaps the other's MFMAs.
-// Measured on MI355X, B4 H32 S8192 D128 causal: 2.30 ms (957 TFLOP/s
-// effective), vs 472 TFLOP/s for PyTorch's SDPA on the same box.
+//   * ~200 VGPRs and 64 KiB of LDS, so two 4-wavefront workgroups share a CU
+//     (the LDS is the limit): one wavefront's softmax VALU work overlaps
+//     the other's MFMAs.
+// Measured on MI355X, B4 H32 S8192 D128 causal: 2.21-2.42 ms (910-994 TFLOP/s
+// effective; the lower figure under sustained load), vs 472 TFLOP/s for
+// PyTorch's SDPA on the same box.
 // ---------------------------------------------------------------------------
 
 namespace dma {

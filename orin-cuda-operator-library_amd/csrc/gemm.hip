@@ -310,8 +310,9 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 //     matrix cores (sched_barrier keeps that order);
 //   * M / N edges: source rows / columns are clamped into the matrix (their
 //     results are never stored), stores are masked.
-// Measured on MI355X (8192^3): 1.01-1.07 PFLOP/s, 84-88% of hipBLASLt's
-// fp16 GEMM on the same box (1.21 PFLOP/s).
+// Measured on MI355X (8192^3): 1.01-1.16 PFLOP/s (the lower figures under
+// sustained load), 84-96% of hipBLASLt's fp16 GEMM on the same boxes
+// (1.21 PFLOP/s).
 // ---------------------------------------------------------------------------
 
 namespace dma {
