@@ -25,6 +25,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <iterator>
 #include <map>
 #include <string>
 #include <vector>
@@ -466,6 +467,12 @@ int main(int argc, char** argv) {
     return 2;
   }
   const std::string op = argv[1];
+  static const char* const kOps[] = {"reduce",  "softmax",  "transpose",     "rmsnorm",
+                                     "gemm_f32", "gemm_f16", "attention_f32", "attention_f16"};
+  if (std::find(std::begin(kOps), std::end(kOps), op) == std::end(kOps)) {
+    std::fprintf(stderr, "unknown op: %s\n", op.c_str());  // before any HIP call
+    return 2;
+  }
   const Options o = parse(argc, argv);
   const int warmup = static_cast<int>(o.get("warmup", 10));
   const int repeat = static_cast<int>(o.get("repeat", 30));
@@ -480,7 +487,6 @@ int main(int argc, char** argv) {
   else if (op == "gemm_f16") rc = run_gemm(o, true, s, warmup, repeat);
   else if (op == "attention_f32") rc = run_attention(o, false, s, warmup, repeat);
   else if (op == "attention_f16") rc = run_attention(o, true, s, warmup, repeat);
-  else std::fprintf(stderr, "unknown op: %s\n", op.c_str());
   RUN_HIP(hipStreamDestroy(s));
   return rc;
 }
