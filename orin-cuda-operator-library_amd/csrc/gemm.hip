@@ -13,9 +13,10 @@
 //     fill, any shape and alignment (the 4095^3 edge case runs on MFMA too).
 //
 // Register-staged tiling (gemm_mfma_kernel, both precisions):
-//   * 256 x 256 C tile per 256-thread workgroup; 2 x 2 wavefronts, each
-//     owning a 128 x 128 sub-tile = 4 x 4 MFMA 32x32 blocks (256 fp32
-//     accumulators per lane, held in AGPR/VGPR at one wave per SIMD);
+//   * 256 x 256 C tile per workgroup. fp16: 2 x 2 wavefronts (256 threads),
+//     each owning a 128 x 128 sub-tile = 4 x 4 MFMA 32x32 blocks (256 fp32
+//     accumulators per lane, one wave per SIMD). fp32: 2 x 4 wavefronts
+//     (512 threads) of 128 x 64, two waves per SIMD (WaveLayout below);
 //   * K step of 128 bytes per row (64 fp16 or 32 fp32): both operands are
 //     kept "k-contiguous" in LDS (A as [m][k], B transposed to [n][k]) so
 //     every MFMA operand is one ds_read_b128;
@@ -51,13 +52,8 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;
 constexpr int kBM = 256;
 constexpr int kBN = 256;
-constexpr int kWaveM = 128;
-constexpr int kWaveN = 128;
-constexpr int kFragsM = kWaveM / 32;  // 4
-constexpr int kFragsN = kWaveN / 32;  // 4
 constexpr int kRowBytes = 128;        // one K step of one row
 constexpr int kChunksPerRow = kRowBytes / 16;
 constexpr int kPitch = kRowBytes + 16;  // padded LDS row
@@ -93,17 +89,45 @@ struct Precision<float> {
   }
 };
 
-template <typename T, bool kVector>
+// Wavefront layout of the register-staged kernel: WM x WN wavefronts over
+// the 256 x 256 C tile. fp16 uses 2 x 2 wavefronts of 128 x 128 (one per
+// SIMD); fp32 uses 2 x 4 of 128 x 64, two per SIMD, whose second wavefront
+// covers the first one's staging and barrier waits (4096^3: 133.1 -> 135.5
+// TFLOP/s, results bit-identical).
+template <int WM, int WN>
+struct WaveLayout {
+  static constexpr int kWM = WM;
+  static constexpr int kWN = WN;
+  static constexpr int kThreads = 64 * WM * WN;
+  static constexpr int kWaveM = kBM / WM;
+  static constexpr int kWaveN = kBN / WN;
+  static constexpr int kFragsM = kWaveM / 32;
+  static constexpr int kFragsN = kWaveN / 32;
+  static constexpr int kWavesPerSimd = WM * WN / 4;
+};
+
+template <typename T>
+struct LayoutFor {
+  using type = WaveLayout<2, 2>;
+};
+template <>
+struct LayoutFor<float> {
+  using type = WaveLayout<2, 4>;
+};
+
+template <typename T, bool kVector, int kThreads>
 struct Stager {
   using P = Precision<T>;
   using Chunk = typename P::Chunk;
   static constexpr int E = P::kChunkElems;
   static constexpr int kBK = kRowBytes / sizeof(T);  // K elements per step
   // A: kBM rows x kChunksPerRow chunks; each thread stages kAChunks.
-  static constexpr int kAChunks = kBM * kChunksPerRow / kThreads;  // 8
+  static constexpr int kAChunks = kBM * kChunksPerRow / kThreads;
   // B: E x E element blocks (E k-rows x one n-chunk); kBBlocks per thread.
-  static constexpr int kBBlocks =
-      (kBK / E) * (kBN / E) / kThreads;  // fp16: 1, fp32: 2
+  static constexpr int kBBlocks = (kBK / E) * (kBN / E) / kThreads;
+  static_assert(kAChunks * kThreads == kBM * kChunksPerRow &&
+                    kBBlocks >= 1 && kBBlocks * kThreads == (kBK / E) * (kBN / E),
+                "staging work must divide evenly over the workgroup");
 
   Chunk a[kAChunks];
   Chunk b[kBBlocks][E];
@@ -198,13 +222,18 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n,
   *tn = in_group / rows_in_group;
 }
 
-template <typename T, bool kVector>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <typename T, bool kVector, typename L = typename LayoutFor<T>::type>
+__global__ __launch_bounds__(L::kThreads)
+__attribute__((amdgpu_waves_per_eu(L::kWavesPerSimd, L::kWavesPerSimd)))
 void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
                       float* __restrict__ C, int M, int N, int K, int ldb) {
   using P = Precision<T>;
   using Chunk = typename P::Chunk;
-  using S = Stager<T, kVector>;
+  using S = Stager<T, kVector, L::kThreads>;
+  constexpr int kWaveM = L::kWaveM;
+  constexpr int kWaveN = L::kWaveN;
+  constexpr int kFragsM = L::kFragsM;
+  constexpr int kFragsN = L::kFragsN;
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
   const int tiles_m = (M + kBM - 1) / kBM;
@@ -216,8 +245,8 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 
   const int lane = threadIdx.x % opl::kWaveSize;
   const int wave = threadIdx.x / opl::kWaveSize;
-  const int wm = wave / 2;
-  const int wn = wave % 2;
+  const int wm = wave / L::kWN;
+  const int wn = wave % L::kWN;
   const int half = lane / 32;
   const int l32 = lane % 32;
 
@@ -1076,7 +1105,7 @@ hipError_t launch_gemm(const T* a, const T* b, float* c, int m, int n, int k,
   const long long tiles = static_cast<long long>((m + kBM - 1) / kBM) *
                           ((n + kBN - 1) / kBN);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>(tiles)), block(kThreads);
+  const dim3 grid(static_cast<unsigned>(tiles)), block(LayoutFor<T>::type::kThreads);
   const bool vector_ok = k % E == 0 && n % E == 0 && opl::aligned16(a) &&
                          opl::aligned16(b);
   if (vector_ok) {
