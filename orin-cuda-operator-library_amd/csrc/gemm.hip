@@ -320,6 +320,9 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 //     (N), each owning 128 x 64 = 4 x 2 MFMA 32x32x16 blocks (128 fp32
 //     accumulators, so two wavefronts fit per SIMD and one's LDS waits are
 //     covered by the other's MFMAs);
+//   * grids of fewer than 160 such tiles (medium M or N) use 128 x 128
+//     tiles instead: 4 wavefronts of 64 x 64, four times the workgroups,
+//     about 2x faster where 256 x 256 tiles would leave most CUs idle;
 //   * A and B are copied global -> LDS by buffer loads with the lds
 //     modifier (each lane writes 16 bytes at LDS base + 16 * lane) from
 //     per-step scalar bases, so operands never pass through VGPRs and no
@@ -349,30 +352,55 @@ namespace dma {
 typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
 #define OPL_LDS __attribute__((address_space(3)))
 
-constexpr int kWM = 2, kWN = 4;
-constexpr int kThreads = 64 * kWM * kWN;  // 512
-constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kFM = kBM / kWM / 32;  // 4
-constexpr int kFN = kBN / kWN / 32;  // 2
-constexpr int kABytes = kBM * kBK * 2;  // 32 KiB, rows of 128 B
-constexpr int kBBytes = kBK * kBN * 2;  // 32 KiB, rows of 512 B
-constexpr int kStage = kABytes + kBBytes;
-constexpr int kCopies = kABytes / 16 / kThreads;  // DMA chunks per thread per operand (4)
+// C tile configurations. BM x BN per workgroup, WM x WN wavefronts of
+// (BM / WM) x (BN / WN); K steps of 64. A rows in LDS are 128 bytes, B rows
+// 2 * BN bytes (BN / 8 16-byte chunks).
+template <int BM, int BN, int WM, int WN>
+struct Tile {
+  static constexpr int kBM = BM, kBN = BN, kBK = 64;
+  static constexpr int kWM = WM, kWN = WN;
+  static constexpr int kThreads = 64 * WM * WN;
+  static constexpr int kFM = BM / WM / 32;
+  static constexpr int kFN = BN / WN / 32;
+  static constexpr int kABytes = BM * kBK * 2;
+  static constexpr int kBBytes = kBK * BN * 2;
+  static constexpr int kBRowBytes = BN * 2;
+  static constexpr int kBChunks = BN / 8;
+  static constexpr int kStage = kABytes + kBBytes;
+  // DMA chunks per thread per operand.
+  static constexpr int kCopies = kABytes / 16 / kThreads;
+  static_assert(kABytes == kBBytes && kCopies * 16 * kThreads == kABytes,
+                "both operand tiles split evenly into 16-byte copies");
+  static_assert(64 % kBChunks == 0, "a wavefront copies whole B rows");
+};
+// 256 x 256: 8 wavefronts of 128 x 64, for grids that fill the GPU.
+using BigTile = Tile<256, 256, 2, 4>;
+// 128 x 128: 4 wavefronts of 64 x 64, four times the workgroups for the
+// same C, for grids that would leave CUs idle with BigTile.
+using SmallTile = Tile<128, 128, 2, 2>;
+constexpr int kBK = 64;  // K step of every tile configuration
 
 __device__ __forceinline__ int swizzle_a(int m) { return (m >> 1) & 7; }
 __device__ __forceinline__ int swizzle_b(int k) { return 4 * (k & 3); }
 
+template <typename Cfg>
 struct Fragments {
-  half8 a[kFM];
-  half8 b[kFN];
+  half8 a[Cfg::kFM];
+  half8 b[Cfg::kFN];
 };
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <typename Cfg>
+__global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
                          const _Float16* __restrict__ B,
                          float* __restrict__ C, int M, int N, int K, int ldb) {
-  __shared__ __attribute__((aligned(1024))) unsigned char stage0[kStage];
-  __shared__ __attribute__((aligned(1024))) unsigned char stage1[kStage];
+  constexpr int kBM = Cfg::kBM, kBN = Cfg::kBN, kBK = Cfg::kBK;
+  constexpr int kWM = Cfg::kWM, kWN = Cfg::kWN;
+  constexpr int kFM = Cfg::kFM, kFN = Cfg::kFN;
+  constexpr int kABytes = Cfg::kABytes, kCopies = Cfg::kCopies;
+  constexpr int kBChunks = Cfg::kBChunks;
+  __shared__ __attribute__((aligned(1024))) unsigned char stage0[Cfg::kStage];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage1[Cfg::kStage];
 
   const int tiles_m = (M + kBM - 1) / kBM;
   const int tiles_n = (N + kBN - 1) / kBN;
@@ -402,8 +430,8 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
     const int m = slot / 8;
     const int chunk = (slot % 8) ^ swizzle_a(m);
     a_dma[j] = (min(m0 + m, M - 1) - m0) * K * 2 + 16 * chunk;
-    const int kk = (wave * kCopies + j) * 2 + lane / 32;
-    const int col = n0 + 8 * ((lane % 32) ^ swizzle_b(kk));
+    const int kk = (wave * kCopies + j) * (64 / kBChunks) + lane / kBChunks;
+    const int col = n0 + 8 * ((lane % kBChunks) ^ swizzle_b(kk));
     b_dma[j] = kk * ldb * 2 + (min(col, ldb - 8) - n0) * 2;
   }
   // Bytes from each step's base to the end of its operand, capped at the
@@ -449,7 +477,7 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
       for (int r = 0; r < 2; ++r) {
         const int n = wn * (kBN / kWN) + 32 * tj + 16 * (group % 2) + 4 * (gl % 4);
         const int k = 16 * s + 8 * (group / 2) + 4 * r + gl / 4;
-        b_off[tj][s][r] = kABytes + k * 512 +
+        b_off[tj][s][r] = kABytes + k * Cfg::kBRowBytes +
                           (((n / 8) ^ swizzle_b(k)) * 16) + (n % 8) * 2;
       }
 
@@ -461,7 +489,7 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  auto load = [&](const unsigned char* st, int s, Fragments& f) {
+  auto load = [&](const unsigned char* st, int s, Fragments<Cfg>& f) {
 #pragma unroll
     for (int ti = 0; ti < kFM; ++ti)
       f.a[ti] = *reinterpret_cast<const half8*>(st + a_off[ti][s]);
@@ -480,7 +508,7 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
       f.b[tj] = b;
     }
   };
-  auto mma = [&](const Fragments& f) {
+  auto mma = [&](const Fragments<Cfg>& f) {
 #pragma unroll
     for (int ti = 0; ti < kFM; ++ti)
 #pragma unroll
@@ -493,7 +521,7 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   auto tile = [&](const unsigned char* cur, unsigned char* nxt, int step) {
     if (step + 1 < steps) issue(nxt, (step + 1) * kBK);
     __builtin_amdgcn_sched_barrier(0);
-    Fragments f0, f1;
+    Fragments<Cfg> f0, f1;
     load(cur, 0, f0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1122,14 +1150,31 @@ hipError_t launch_gemm(const T* a, const T* b, float* c, int m, int n, int k,
   return hipGetLastError();
 }
 
+template <typename Cfg>
+hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
+                            int m, int n, int k, int ldb, hipStream_t stream) {
+  const long long tiles = static_cast<long long>((m + Cfg::kBM - 1) / Cfg::kBM) *
+                          ((n + Cfg::kBN - 1) / Cfg::kBN);
+  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+  dma::gemm_f16_dma_kernel<Cfg><<<dim3(static_cast<unsigned>(tiles)), dim3(Cfg::kThreads),
+                                  0, stream>>>(a, b, c, m, n, k, ldb);
+  return hipGetLastError();
+}
+
+// Grids of fewer 256 x 256 tiles than this run on 128 x 128 tiles. Measured
+// on MI355X (us, 256 x 256 vs 128 x 128 tiles): 1000 x 4096 x 4096 (64
+// tiles) 85.9 vs 45.9; 2048 x 4096 x 4096 (128) 89.1 vs 69.7; 2304 x 5120 x
+// 4096 (180) 102.8 vs 110.0; 4096^3 (256) 121.1 vs 136.5.
+constexpr long long kSmallGridTiles = 160;
+
 hipError_t launch_gemm_f16_dma(const _Float16* a, const _Float16* b, float* c,
                                int m, int n, int k, int ldb, hipStream_t stream) {
-  const long long tiles = static_cast<long long>((m + dma::kBM - 1) / dma::kBM) *
-                          ((n + dma::kBN - 1) / dma::kBN);
-  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-  dma::gemm_f16_dma_kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(dma::kThreads),
-                             0, stream>>>(a, b, c, m, n, k, ldb);
-  return hipGetLastError();
+  const long long big_tiles =
+      static_cast<long long>((m + dma::BigTile::kBM - 1) / dma::BigTile::kBM) *
+      ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
+  if (big_tiles < kSmallGridTiles)
+    return launch_dma_tiles<dma::SmallTile>(a, b, c, m, n, k, ldb, stream);
+  return launch_dma_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, stream);
 }
 
 }  // namespace
