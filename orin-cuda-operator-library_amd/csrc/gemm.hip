@@ -52,15 +52,9 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 256;
-constexpr int kBN = 256;
 constexpr int kRowBytes = 128;        // one K step of one row
 constexpr int kChunksPerRow = kRowBytes / 16;
 constexpr int kPitch = kRowBytes + 16;  // padded LDS row
-constexpr int kTileABytes = kBM * kPitch;
-constexpr int kTileBBytes = kBN * kPitch;
-constexpr int kStageBytes = kTileABytes + kTileBBytes;
-constexpr int kLdsBytes = 2 * kStageBytes;  // 147456 of 163840
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;
 
@@ -89,44 +83,59 @@ struct Precision<float> {
   }
 };
 
-// Wavefront layout of the register-staged kernel: WM x WN wavefronts over
-// the 256 x 256 C tile. fp16 uses 2 x 2 wavefronts of 128 x 128 (one per
-// SIMD); fp32 uses 2 x 4 of 128 x 64, two per SIMD, whose second wavefront
-// covers the first one's staging and barrier waits (4096^3: 133.1 -> 135.5
-// TFLOP/s, results bit-identical).
-template <int WM, int WN>
+// Tile and wavefront layout of the register-staged kernel: a BM x BN C tile
+// per workgroup, WM x WN wavefronts, WavesPerSimd wavefronts resident per
+// SIMD (the register budget follows from it).
+//   * fp16: 256 x 256, 2 x 2 wavefronts of 128 x 128, one per SIMD;
+//   * fp32: 256 x 256, 2 x 4 wavefronts of 128 x 64, two per SIMD, whose
+//     second wavefront covers the first one's staging and barrier waits
+//     (4096^3: 133.1 -> 135.5 TFLOP/s, results bit-identical);
+//   * fp32 on grids that 256 x 256 tiles would leave mostly idle:
+//     128 x 128, 2 x 2 wavefronts of 64 x 64, two workgroups per CU.
+template <int WM, int WN, int BM, int BN, int WavesPerSimd>
 struct WaveLayout {
   static constexpr int kWM = WM;
   static constexpr int kWN = WN;
+  static constexpr int kBM = BM;
+  static constexpr int kBN = BN;
   static constexpr int kThreads = 64 * WM * WN;
-  static constexpr int kWaveM = kBM / WM;
-  static constexpr int kWaveN = kBN / WN;
+  static constexpr int kWaveM = BM / WM;
+  static constexpr int kWaveN = BN / WN;
   static constexpr int kFragsM = kWaveM / 32;
   static constexpr int kFragsN = kWaveN / 32;
-  static constexpr int kWavesPerSimd = WM * WN / 4;
+  static constexpr int kWavesPerSimd = WavesPerSimd;
+  static constexpr int kTileABytes = BM * kPitch;
+  static constexpr int kTileBBytes = BN * kPitch;
+  static constexpr int kStageBytes = kTileABytes + kTileBBytes;
+  static constexpr int kLdsBytes = 2 * kStageBytes;
 };
+
+using F16Layout = WaveLayout<2, 2, 256, 256, 1>;
+using F32Layout = WaveLayout<2, 4, 256, 256, 2>;
+using F32SmallLayout = WaveLayout<2, 2, 128, 128, 2>;
 
 template <typename T>
 struct LayoutFor {
-  using type = WaveLayout<2, 2>;
+  using type = F16Layout;
 };
 template <>
 struct LayoutFor<float> {
-  using type = WaveLayout<2, 4>;
+  using type = F32Layout;
 };
 
-template <typename T, bool kVector, int kThreads>
+template <typename T, bool kVector, typename L>
 struct Stager {
   using P = Precision<T>;
   using Chunk = typename P::Chunk;
   static constexpr int E = P::kChunkElems;
   static constexpr int kBK = kRowBytes / sizeof(T);  // K elements per step
-  // A: kBM rows x kChunksPerRow chunks; each thread stages kAChunks.
-  static constexpr int kAChunks = kBM * kChunksPerRow / kThreads;
+  static constexpr int kThreads = L::kThreads;
+  // A: BM rows x kChunksPerRow chunks; each thread stages kAChunks.
+  static constexpr int kAChunks = L::kBM * kChunksPerRow / kThreads;
   // B: E x E element blocks (E k-rows x one n-chunk); kBBlocks per thread.
-  static constexpr int kBBlocks = (kBK / E) * (kBN / E) / kThreads;
-  static_assert(kAChunks * kThreads == kBM * kChunksPerRow &&
-                    kBBlocks >= 1 && kBBlocks * kThreads == (kBK / E) * (kBN / E),
+  static constexpr int kBBlocks = (kBK / E) * (L::kBN / E) / kThreads;
+  static_assert(kAChunks * kThreads == L::kBM * kChunksPerRow &&
+                    kBBlocks >= 1 && kBBlocks * kThreads == (kBK / E) * (L::kBN / E),
                 "staging work must divide evenly over the workgroup");
 
   Chunk a[kAChunks];
@@ -181,7 +190,7 @@ struct Stager {
   __device__ __forceinline__ void store(unsigned char* stage) const {
     const int tid = threadIdx.x;
     unsigned char* sa = stage;
-    unsigned char* sb = stage + kTileABytes;
+    unsigned char* sb = stage + L::kTileABytes;
 #pragma unroll
     for (int i = 0; i < kAChunks; ++i) {
       const int q = tid + kThreads * i;
@@ -229,12 +238,16 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
                       float* __restrict__ C, int M, int N, int K, int ldb) {
   using P = Precision<T>;
   using Chunk = typename P::Chunk;
-  using S = Stager<T, kVector, L::kThreads>;
+  using S = Stager<T, kVector, L>;
+  constexpr int kBM = L::kBM;
+  constexpr int kBN = L::kBN;
+  constexpr int kTileABytes = L::kTileABytes;
+  constexpr int kStageBytes = L::kStageBytes;
   constexpr int kWaveM = L::kWaveM;
   constexpr int kWaveN = L::kWaveN;
   constexpr int kFragsM = L::kFragsM;
   constexpr int kFragsN = L::kFragsN;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds[L::kLdsBytes];
 
   const int tiles_m = (M + kBM - 1) / kBM;
   const int tiles_n = (N + kBN - 1) / kBN;
@@ -1126,28 +1139,58 @@ hipError_t pad_operands(const T* a, const T* b, int m, int n, int k, int k_mult,
   return hipGetLastError();
 }
 
+// One launch of gemm_mfma_kernel with tile layout L (general or 16-byte
+// vector staging).
+template <typename T, typename L>
+hipError_t launch_generic(bool vector, const T* a, const T* b, float* c, int m,
+                          int n, int k, int ldb, hipStream_t stream) {
+  const long long tiles = static_cast<long long>((m + L::kBM - 1) / L::kBM) *
+                          ((n + L::kBN - 1) / L::kBN);
+  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(tiles)), block(L::kThreads);
+  if (vector)
+    gemm_mfma_kernel<T, true, L><<<grid, block, 0, stream>>>(a, b, c, m, n, k, ldb);
+  else
+    gemm_mfma_kernel<T, false, L><<<grid, block, 0, stream>>>(a, b, c, m, n, k, ldb);
+  return hipGetLastError();
+}
+
+// fp32 grids of fewer 256 x 256 tiles than this run on 128 x 128 tiles: a
+// 256 x 256 workgroup takes a whole CU for ~1 ms at K = 4096 whatever the
+// grid, so below one tile per CU the smaller tiles win. Measured on MI355X
+// (us, 256 x 256 vs 128 x 128): 1000 x 4096 x 4096 (64 tiles) 1006 vs 302;
+// 2048 x 4096 x 4096 (128) 1007 vs 547; 3072 x 4096 x 4096 (192) 1009 vs
+// 830; 4096^3 (256) 1010 vs 1078.
+constexpr long long kSmallGridTilesF32 = 256;
+
+template <typename T>
+hipError_t launch_generic_for(bool vector, const T* a, const T* b, float* c, int m,
+                              int n, int k, int ldb, hipStream_t stream) {
+  using L = typename LayoutFor<T>::type;
+  if constexpr (std::is_same<T, float>::value) {
+    const long long big_tiles = static_cast<long long>((m + L::kBM - 1) / L::kBM) *
+                                ((n + L::kBN - 1) / L::kBN);
+    if (big_tiles < kSmallGridTilesF32)
+      return launch_generic<T, F32SmallLayout>(vector, a, b, c, m, n, k, ldb, stream);
+  }
+  return launch_generic<T, L>(vector, a, b, c, m, n, k, ldb, stream);
+}
+
 template <typename T>
 hipError_t launch_gemm(const T* a, const T* b, float* c, int m, int n, int k,
                        hipStream_t stream) {
   constexpr int E = Precision<T>::kChunkElems;
-  const long long tiles = static_cast<long long>((m + kBM - 1) / kBM) *
-                          ((n + kBN - 1) / kBN);
-  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>(tiles)), block(LayoutFor<T>::type::kThreads);
   const bool vector_ok = k % E == 0 && n % E == 0 && opl::aligned16(a) &&
                          opl::aligned16(b);
-  if (vector_ok) {
-    gemm_mfma_kernel<T, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k, n);
-  } else if (worth_padding(m, n, k)) {
+  if (vector_ok) return launch_generic_for<T>(true, a, b, c, m, n, k, n, stream);
+  if (worth_padding(m, n, k)) {
     PaddedOperands p;
     const hipError_t status = pad_operands<T>(a, b, m, n, k, E, E, stream, &p);
     if (status != hipSuccess) return status;
-    gemm_mfma_kernel<T, true><<<grid, block, 0, stream>>>(
-        static_cast<const T*>(p.a), static_cast<const T*>(p.b), c, m, n, p.k, p.ldb);
-  } else {
-    gemm_mfma_kernel<T, false><<<grid, block, 0, stream>>>(a, b, c, m, n, k, n);
+    return launch_generic_for<T>(true, static_cast<const T*>(p.a),
+                                 static_cast<const T*>(p.b), c, m, n, p.k, p.ldb, stream);
   }
-  return hipGetLastError();
+  return launch_generic_for<T>(false, a, b, c, m, n, k, n, stream);
 }
 
 template <typename Cfg>

@@ -312,19 +312,24 @@ def test_gemm_padded_operands(hip, mnk, offset, dtype):
     assert np.isfinite(y).all()
 
 
-@pytest.mark.parametrize("mnk", [(520, 2056, 1024), (1000, 4096, 512), (136, 8192, 256)])
-def test_gemm_f16_small_grid_tiles(hip, mnk):
+@pytest.mark.parametrize("mnk", [(520, 2056, 1024), (1000, 4096, 512), (136, 8192, 256),
+                                 (1000, 1028, 520)])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_gemm_small_grid_tiles(hip, mnk, dtype):
     """Grids too small for 256 x 256 tiles to fill the GPU run on 128 x 128
-    tiles: ragged last tile rows / columns (8 wide), every row checked."""
+    tiles: ragged last tile rows / columns (8 or 4 wide), every row checked."""
     m, n, k = mnk
-    a = oracle.to_f16_bits(oracle.uniform(660 + m, (m, k)))
-    b = oracle.to_f16_bits(oracle.uniform(661 + n, (k, n)))
-    y = hip.gemm_f16(a, b)
-    rows = np.arange(m) if m * n * k <= 2 ** 31 else np.unique(
-        np.concatenate([np.arange(8), np.arange(m - 8, m),
-                        np.random.default_rng(m).integers(0, m, 64)]))
-    ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b), rows)
-    assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    a = oracle.uniform(660 + m, (m, k))
+    b = oracle.uniform(661 + n, (k, n))
+    if dtype == "f16":
+        a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(a, b)
+        ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b))
+        assert np.max(np.abs(y - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b)
+        ref = oracle.gemm(a, b)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
     assert np.isfinite(y).all()
 
 
