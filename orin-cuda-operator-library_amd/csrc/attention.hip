@@ -623,13 +623,14 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
           if (key > my_row) s[e] = -INFINITY;
         }
       };
-      // Row max of a half's raw scores, both lane halves combined
-      // (v_maximum3_f32: 8 instructions for 16 values).
-      auto half_max = [&](const floatx16& s) {
+      // Max of this lane's 16 raw scores of a half (v_maximum3_f32: 8
+      // instructions). The row's other 16 scores sit in lane l ^ 32; the
+      // two are combined only when the max has to move (move_max).
+      auto lane_max = [&](const floatx16& s) {
         float m = s[0];
 #pragma unroll
         for (int e = 1; e < 16; ++e) m = __builtin_elementwise_maximum(m, s[e]);
-        return opl::max_lane_xor32(m);
+        return m;
       };
       // Lazy rescaling: the running max m (log2 units) only moves when a
       // row's max exceeds it by more than kLazyLog2, so p = 2^(x - m) stays
@@ -637,10 +638,13 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
       // skipped on almost every half-tile. Softmax is shift-invariant: the
       // result is the same up to rounding. The test compares raw scores
       // with move_above = (m + kLazyLog2) / scale, updated when m moves.
-      auto needs_move = [&](float raw) {
-        return __builtin_amdgcn_ballot_w64(raw > move_above) != 0;
+      auto needs_move = [&](float lane_raw) {
+        return __builtin_amdgcn_ballot_w64(lane_raw > move_above) != 0;
       };
-      auto move_max = [&](float raw) {
+      // Wave-uniform branch: every lane runs it, and both lanes of a row
+      // combine their halves, so they move to the same max.
+      auto move_max = [&](float lane_raw) {
+        const float raw = opl::max_lane_xor32(lane_raw);
         const float new_max = fmaxf(row_max, raw * score_scale_log2);
         const float alpha = opl::fast_exp2(row_max - new_max);
         row_max = new_max;
@@ -686,13 +690,13 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
         half8 p0[2], p1[2];
         floatx16 s0 = scores(0);
         if constexpr (kMasked) mask(s0, 0);
-        const float c0 = half_max(s0);
+        const float c0 = lane_max(s0);
         if (needs_move(c0)) move_max(c0);
         floatx16 s1 = scores(1);
         row_sum += exponentiate(s0, p0);
         accumulate(0, p0);
         if constexpr (kMasked) mask(s1, 1);
-        const float c1 = half_max(s1);
+        const float c1 = lane_max(s1);
         float ps1 = exponentiate(s1, p1);
         if (needs_move(c1)) {
           move_max(c1);  // after P.V of half 0, which used the old max
