@@ -45,6 +45,7 @@
 
 #include "common.hpp"
 #include "operatorlib/operatorlib_c.h"
+#include "scratch.hpp"
 #include "validate.hpp"
 
 namespace {
@@ -231,11 +232,12 @@ struct KvStager {
   }
 };
 
-template <typename T, int NDT, bool kVector>
+template <typename T, int NDT, bool kVector, bool kSplit>
 __global__ __launch_bounds__(kThreads) void attention_mfma_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     float* __restrict__ O, int BH, int S, int D, int causal,
-    float score_scale_log2) {
+    float score_scale_log2, int splits, float* __restrict__ part_o,
+    float* __restrict__ part_ml) {
   using L = AttnLayout<T, NDT>;
   using Pr = AttnPrec<T>;
   using Chunk = typename Pr::Chunk;
@@ -244,9 +246,14 @@ __global__ __launch_bounds__(kThreads) void attention_mfma_kernel(
 
   // Heaviest query blocks first; all blocks of one head map to one XCD
   // (launch index modulo 8) whenever BH is a multiple of 8.
+  // With splits > 1 (small grids) the key tiles of a query block are dealt
+  // to `splits` workgroups; each writes its unnormalised O, row max and row
+  // sum to part_o / part_ml and attention_combine_kernel merges them.
   const int q_blocks = (S + kBlockRows - 1) / kBlockRows;
-  const int qb = q_blocks - 1 - static_cast<int>(blockIdx.x / BH);
-  const int bh = static_cast<int>(blockIdx.x % BH);
+  const unsigned item = kSplit ? blockIdx.x / splits : blockIdx.x;
+  const int split = kSplit ? static_cast<int>(blockIdx.x % splits) : 0;
+  const int qb = q_blocks - 1 - static_cast<int>(item / BH);
+  const int bh = static_cast<int>(item % BH);
   const int q0 = qb * kBlockRows;
 
   const int lane = threadIdx.x % opl::kWaveSize;
@@ -276,16 +283,22 @@ __global__ __launch_bounds__(kThreads) void attention_mfma_kernel(
   float row_sum = 0.0f;      // this lane's half of the row sum
 
   const int visible_end = causal ? min(S, q0 + kBlockRows) : S;
-  const int tiles = (visible_end + L::kKeys - 1) / L::kKeys;
+  const int all_tiles = (visible_end + L::kKeys - 1) / L::kKeys;
+  // This workgroup's tiles: [tile0, tile0 + tiles).
+  const int per_split = kSplit ? (all_tiles + splits - 1) / splits : all_tiles;
+  const int tile0 = kSplit ? min(all_tiles, split * per_split) : 0;
+  const int tiles = kSplit ? min(all_tiles, tile0 + per_split) - tile0 : all_tiles;
 
   KvStager<T, NDT, kVector> stager;
-  stager.load(kh, vh, 0, S, D);
-  stager.store(lds);
+  if (!kSplit || tiles > 0) {  // a split may own no tile of a causal block
+    stager.load(kh, vh, tile0 * L::kKeys, S, D);
+    stager.store(lds);
+  }
   __syncthreads();
 
   for (int tile = 0; tile < tiles; ++tile) {
     const unsigned char* stage = lds + (tile & 1) * L::kStageBytes;
-    const int key0 = tile * L::kKeys;
+    const int key0 = (tile0 + tile) * L::kKeys;
     if (tile + 1 < tiles) stager.load(kh, vh, key0 + L::kKeys, S, D);
 
     const bool wave_active = !causal || key0 <= wave_row0 + kRowsPerWave - 1;
@@ -385,9 +398,23 @@ __global__ __launch_bounds__(kThreads) void attention_mfma_kernel(
   // ---- normalise and store: lane holds O^T[d][row] for d = 32dt + 8(e/4) +
   // 4*half + e%4, i.e. four runs of 4 consecutive dims per tile ------------
   const float total = opl::sum_lane_xor32(row_sum);
-  const float inv = 1.0f / total;
+  float inv = 1.0f / total;
+  float* out_base = O;
+  if constexpr (kSplit) {
+    // Partial: unnormalised O, then (max, sum) of the row. A split that saw
+    // no visible key of a row leaves max -FLT_MAX, sum 0 and O 0, which
+    // the combine weighs by 0.
+    inv = 1.0f;
+    out_base = part_o + static_cast<std::size_t>(split) * BH * S * D;
+    if (my_row < S && half == 0) {
+      float* ml = part_ml + (static_cast<std::size_t>(split) * BH * S +
+                             static_cast<std::size_t>(bh) * S + my_row) * 2;
+      ml[0] = row_max;
+      ml[1] = total;
+    }
+  }
   if (my_row < S) {
-    float* orow = O + head + static_cast<std::size_t>(my_row) * D;
+    float* orow = out_base + head + static_cast<std::size_t>(my_row) * D;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
@@ -408,20 +435,93 @@ __global__ __launch_bounds__(kThreads) void attention_mfma_kernel(
   }
 }
 
+// out[row][d] = sum_s 2^(m_s - m) O_s[row][d] / sum_s 2^(m_s - m) l_s, with
+// m = max_s m_s, over the splits in order (deterministic). One thread per
+// row and 4 consecutive dims (d0 < D).
+__global__ __launch_bounds__(256) void attention_combine_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    float* __restrict__ out, long long rows, int D, int splits) {
+  const int quads = (D + 3) / 4;
+  const long long i = blockIdx.x * 256LL + threadIdx.x;
+  if (i >= rows * quads) return;
+  const long long row = i / quads;
+  const int d0 = static_cast<int>(i % quads) * 4;
+  float m = -FLT_MAX;
+  for (int sp = 0; sp < splits; ++sp) m = fmaxf(m, part_ml[(sp * rows + row) * 2]);
+  float l = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sp = 0; sp < splits; ++sp) {
+    const float w = opl::fast_exp2(part_ml[(sp * rows + row) * 2] - m);
+    l += w * part_ml[(sp * rows + row) * 2 + 1];
+    const float* o = part_o + (sp * rows + row) * D + d0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (d0 + r < D) acc[r] += w * o[r];
+  }
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (d0 + r < D) out[row * D + d0 + r] = acc[r] * inv;
+}
+
+// Register-staged kernel (one workgroup per CU): small grids deal each
+// query block's keys to `splits` workgroups, as many as keep blocks *
+// splits within kSplitBudget workgroups (one per CU), at most 4; causal
+// grids, whose heaviest blocks set the time, may use twice that budget.
+// Measured on MI355X, fp32 D 128 (us; 1 / 2 / 4 splits): B1 H12 S1024
+// 169.6 / 104.0 / 111.9, causal 171.3 / 100.7 / 66.4; B1 H8 S2048 333.0 /
+// 194.7 / 205.4; B1 H24 S1024 causal 175.1 / 110.7 / 119.3; B2 H12 S1024
+// 175.8 / 198.0 / 174.7.
+constexpr long long kSplitBudget = 256;
+constexpr int kMaxSplits = 4;
+
 template <typename T, int NDT>
-void launch_attention(const T* q, const T* k, const T* v, float* out, int bh,
-                      int s, int d, int causal, bool vector_ok,
-                      hipStream_t stream) {
+hipError_t launch_attention(const T* q, const T* k, const T* v, float* out, int bh,
+                            int s, int d, int causal, bool vector_ok,
+                            hipStream_t stream) {
   const int q_blocks = (s + kBlockRows - 1) / kBlockRows;
   const long long blocks = static_cast<long long>(q_blocks) * bh;
   const float scale = 1.4426950408889634f / sqrtf(static_cast<float>(d));
-  const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
-  if (vector_ok)
-    attention_mfma_kernel<T, NDT, true><<<grid, block, 0, stream>>>(
-        q, k, v, out, bh, s, d, causal, scale);
-  else
-    attention_mfma_kernel<T, NDT, false><<<grid, block, 0, stream>>>(
-        q, k, v, out, bh, s, d, causal, scale);
+  // Key tiles per query block bound the useful split count.
+  const int max_tiles = (s + AttnLayout<T, NDT>::kKeys - 1) / AttnLayout<T, NDT>::kKeys;
+  const long long budget = causal ? 2 * kSplitBudget : kSplitBudget;
+  int splits = static_cast<int>(budget / blocks < kMaxSplits ? budget / blocks : kMaxSplits);
+  if (splits > max_tiles) splits = max_tiles;
+  if (splits < 1) splits = 1;
+  float* part_o = nullptr;
+  float* part_ml = nullptr;
+  if (splits > 1) {
+    const std::size_t rows = static_cast<std::size_t>(bh) * s;
+    void* ws = nullptr;
+    const hipError_t status = opl::workspace_for_stream(
+        stream, static_cast<std::size_t>(splits) * rows * (d + 2) * sizeof(float), &ws);
+    if (status != hipSuccess) return status;
+    part_o = static_cast<float*>(ws);
+    part_ml = part_o + static_cast<std::size_t>(splits) * rows * d;
+  }
+  const dim3 grid(static_cast<unsigned>(blocks * splits)), block(kThreads);
+  if (splits > 1) {
+    if (vector_ok)
+      attention_mfma_kernel<T, NDT, true, true><<<grid, block, 0, stream>>>(
+          q, k, v, out, bh, s, d, causal, scale, splits, part_o, part_ml);
+    else
+      attention_mfma_kernel<T, NDT, false, true><<<grid, block, 0, stream>>>(
+          q, k, v, out, bh, s, d, causal, scale, splits, part_o, part_ml);
+  } else {
+    if (vector_ok)
+      attention_mfma_kernel<T, NDT, true, false><<<grid, block, 0, stream>>>(
+          q, k, v, out, bh, s, d, causal, scale, 1, nullptr, nullptr);
+    else
+      attention_mfma_kernel<T, NDT, false, false><<<grid, block, 0, stream>>>(
+          q, k, v, out, bh, s, d, causal, scale, 1, nullptr, nullptr);
+  }
+  if (splits > 1) {
+    const long long rows = static_cast<long long>(bh) * s;
+    const long long threads = rows * ((d + 3) / 4);
+    attention_combine_kernel<<<dim3(static_cast<unsigned>((threads + 255) / 256)),
+                               dim3(256), 0, stream>>>(part_o, part_ml, out, rows, d,
+                                                        splits);
+  }
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -863,12 +963,11 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
     }
   }
   switch ((head_dim + 31) / 32) {
-    case 1: launch_attention<T, 1>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream); break;
-    case 2: launch_attention<T, 2>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream); break;
-    case 3: launch_attention<T, 3>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream); break;
-    default: launch_attention<T, 4>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream); break;
+    case 1: return launch_attention<T, 1>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream);
+    case 2: return launch_attention<T, 2>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream);
+    case 3: return launch_attention<T, 3>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream);
+    default: return launch_attention<T, 4>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream);
   }
-  return hipGetLastError();
 }
 
 }  // namespace

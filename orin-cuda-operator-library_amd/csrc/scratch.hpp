@@ -26,9 +26,11 @@ constexpr int kReduceMaxBlocks = 1024;
 // current device, allocating it on first use. Thread-safe.
 hipError_t reduce_partials_for_stream(hipStream_t stream, double** out);
 
-// 2. GEMM operand workspace: GEMMs whose operands do not meet the fast
-// kernels' shape / alignment rules are first copied into zero-padded,
-// aligned buffers here. Grow-only: a request larger than the current
+// 2. Operand / partials workspace: GEMMs whose operands do not meet the
+// fast kernels' shape / alignment rules are first copied into zero-padded,
+// aligned buffers here; decode GEMMs keep their split-K partial sums here,
+// and register-staged attention on small grids its per-split partial
+// outputs. Grow-only: a request larger than the current
 // buffer allocates a new one of max(bytes, 2 x current) and retires the old
 // one without freeing it (kernels earlier in the stream may still read it,
 // and freeing would synchronize), so total memory stays under twice the

@@ -54,6 +54,9 @@ def _all_ops(ops, t):
         ops.gemm(t["ah"], t["bh"]),      # zero-padded workspace path
         ops.gemm(t["a1"], t["b1"]),      # skinny path with K splits
         ops.attention(t["q"], t["k"], t["v"], True),
+        # fp32, 8 query blocks: keys split over workgroups, partials in the
+        # workspace, then the combine kernel
+        ops.attention(t["q"].float(), t["k"].float(), t["v"].float(), False),
     ]
 
 
