@@ -665,7 +665,8 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   // costing a v_readfirstlane per copy and tile.
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto issue = [&](unsigned char* st, int key0) {
-    const int tile_bytes = key0 * D * 2;
+    // < head_bytes < 2^32: unsigned, so a head above 2 GiB cannot overflow
+    const unsigned tile_bytes = static_cast<unsigned>(key0) * D * 2u;
 #pragma unroll
     for (int j = 0; j < L::kCopies; ++j)
       opl::buffer_copy16_lds(kh, head_bytes, st + (wave_s * L::kCopies + j) * 1024,

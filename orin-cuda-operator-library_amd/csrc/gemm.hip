@@ -1240,10 +1240,13 @@ extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
   const _Float16* hb = reinterpret_cast<const _Float16*>(b);
   hipStream_t stream = static_cast<hipStream_t>(stream_handle);
   if (skinny::applies(hb, m, n)) return skinny::launch<_Float16>(ha, hb, c, m, n, k, stream);
-  if (k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
+  // The copy kernel's per-lane offsets inside a tile are 32-bit: up to
+  // 255 rows of A (255 * K * 2 bytes) and 64 rows of B (64 * N * 2).
+  const bool dma_offsets_fit = k < (1 << 22) && n < (1 << 24);
+  if (dma_offsets_fit && k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
       opl::aligned16(b))
     return launch_gemm_f16_dma(ha, hb, c, m, n, k, n, stream);
-  if (worth_padding(m, n, k)) {
+  if (dma_offsets_fit && worth_padding(m, n, k)) {
     PaddedOperands p;
     const hipError_t status =
         pad_operands<_Float16>(ha, hb, m, n, k, dma::kBK, 8, stream, &p);
