@@ -32,7 +32,12 @@
 //   * causal: key tiles beyond the workgroup's last row are never loaded,
 //     wavefronts skip tiles beyond their own rows, masks are applied only on
 //     diagonal / ragged tiles; workgroups are issued heaviest-first, and
-//     all workgroups of one head share an XCD (and its L2).
+//     all workgroups of one head share an XCD (and its L2);
+//   * grids too small to fill the GPU split each query block's keys: the
+//     fp16 fast path between two wavefront groups of one workgroup (merged
+//     through LDS), the register-staged kernel over several workgroups
+//     (partials in the stream's workspace, merged by
+//     attention_combine_kernel in split order).
 // Head dims are padded to a multiple of 32 with zeros (any 1 <= D <= 128).
 
 #include <hip/hip_runtime.h>

@@ -4,13 +4,21 @@
 //
 // Reference: operatorlib::gemm_f16 / gemm_f32 (src/gemm.cu:440-479). The
 // reference dispatches between WMMA, cp.async register-tiled and scalar
-// kernels on divisibility; here every path runs on MFMA:
+// kernels on divisibility; here the dispatch is, in order:
+//   * M <= 16 (decode shapes): the skinny kernels (namespace skinny), an
+//     HBM stream over B with split K and an ordered split sum;
 //   * gemm_f16_dma_kernel (fp16, K % 64 == 0, N % 8 == 0, 16-byte aligned
 //     operands): direct global->LDS loads, described before the kernel;
+//     256 x 256 tiles, or 128 x 128 when the grid would leave CUs idle;
+//   * large shapes that miss those rules (e.g. 4095^3): zero-padded copies
+//     of the operands in the stream's workspace, then the fast kernels;
 //   * gemm_mfma_kernel "vector" instance: 16-byte register-staged chunks,
-//     16-byte aligned rows (all fp32 shapes with K, N % 4 == 0);
+//     16-byte aligned rows (all fp32 shapes with K, N % 4 == 0); fp32 uses
+//     128 x 128 tiles on small grids;
 //   * gemm_mfma_kernel "general" instance: element-wise staging with zero
-//     fill, any shape and alignment (the 4095^3 edge case runs on MFMA too).
+//     fill, any shape and alignment.
+// Every path but the vector-ALU skinny kernel (M <= 4 fp16, M <= 8 fp32)
+// runs on the matrix cores.
 //
 // Register-staged tiling (gemm_mfma_kernel, both precisions):
 //   * 256 x 256 C tile per workgroup. fp16: 2 x 2 wavefronts (256 threads),
