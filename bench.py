@@ -432,7 +432,7 @@ def cpu_baseline(oracle, budget_s: float):
     gbps = done * step_bytes / el / 1e9
     return {"value": round(gbps, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{done} full steps (softmax 4096x1024 + rmsnorm 2048x4096) in {el:.1f} s, "
-                      f"oracle/oracle.c single thread, gcc -O2; host {platform.processor() or platform.machine()}, "
+                      f"oracle/oracle.c single thread, gcc -O3; host {platform.processor() or platform.machine()}, "
                       f"nproc {os.cpu_count()}"}
 
 
