@@ -36,6 +36,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 sys.path.insert(0, str(REPO / "orin-cuda-operator-library_amd"))
@@ -436,6 +438,55 @@ def cpu_baseline(oracle, budget_s: float):
                       f"nproc {os.cpu_count()}"}
 
 
+def cpu_ops_baseline(oracle):
+    """Single-threaded oracle timings of every BASELINE config (reported
+    beside the GPU figures, not a target). Bandwidth ops run in full (best
+    of two calls); GEMM times a few rows of A against the full B, attention
+    a few rows of one head against that head's full K and V, and both are
+    scaled to all rows (the sample is named in each entry)."""
+    def timed(fn, reps=2):
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            best = min(best, time.perf_counter() - t0)
+        return best * 1e3
+
+    out = []
+    x = oracle.uniform(21, 16_777_216)
+    out.append(("reduce_sum_f32", [16_777_216], timed(lambda: oracle.reduce_sum(x)), "full"))
+    for shape in ((4096, 1024), (4097, 1023)):
+        x = oracle.normal(22, shape, 0.0, 3.0)
+        out.append(("softmax_f32", list(shape), timed(lambda: oracle.softmax(x)), "full"))
+    for shape in ((2048, 4096), (2047, 4095)):
+        x = oracle.normal(23, shape)
+        w = oracle.uniform(24, shape[1], 0.5, 1.5)
+        out.append(("rmsnorm_f32", list(shape), timed(lambda: oracle.rmsnorm(x, w, 1e-6)), "full"))
+    for shape in ((4096, 4096), (4095, 4097)):
+        x = oracle.uniform(25, shape)
+        out.append(("transpose_f32", list(shape), timed(lambda: oracle.transpose(x)), "full"))
+    for name, size, rows in (("gemm_f32", 4096, 4), ("gemm_f16", 8192, 2)):
+        a = oracle.uniform(26, (rows, size), -1.0, 1.0)
+        b = oracle.uniform(27, (size, size), -1.0, 1.0)
+        ms = timed(lambda: oracle.gemm(a, b), reps=1) * size / rows
+        out.append((name, [size, size, size], ms, f"{rows} rows of A, scaled to {size}"))
+        del a, b
+    for bsz, heads, seq, causal, rows in ((1, 12, 1024, False, 128), (1, 12, 1024, True, 128),
+                                          (4, 32, 8192, True, 16)):
+        q, k, v = (oracle.normal(30 + i, (1, 1, seq, 128)) for i in range(3))
+        # evenly spaced rows: causal row cost grows with the row index
+        rr = (np.arange(rows) * seq) // rows + seq // (2 * rows)
+        hh = np.zeros(rows, dtype=np.int64)
+        ms = timed(lambda: oracle.attention(q, k, v, causal, heads=hh, rows=rr), reps=1)
+        ms *= bsz * heads * seq / rows
+        out.append(("attention_f16", [bsz, heads, seq, 128], ms,
+                    f"{rows} evenly spaced rows of one head, scaled to {bsz * heads * seq} rows"
+                    + (", causal" if causal else "")))
+        del q, k, v
+    return [{"op": n, "shape": sh, "cpu_ms": round(ms, 3), "sample": smp, "cores": 1}
+            for n, sh, ms, smp in out]
+
+
 def torch_cpu_baseline(torch, budget_s: float):
     import numpy as np
     threads = torch.get_num_threads()
@@ -523,9 +574,17 @@ def main():
 
     cpu = None
     extra_cpu = None
+    cpu_ops = None
     if not args.no_cpu:
         cpu = cpu_baseline(oracle, args.cpu_seconds)
         extra_cpu = torch_cpu_baseline(torch, min(5.0, args.cpu_seconds))
+        cpu_ops = cpu_ops_baseline(oracle)
+        # GPU / CPU-oracle ratio on the matching op entries
+        for c in cpu_ops:
+            for o in ops:
+                if o["op"] == c["op"] and o["shape"] == c["shape"] and o.get("ms"):
+                    o["cpu_oracle_ms"] = c["cpu_ms"]
+                    o["speedup_vs_cpu_oracle"] = round(c["cpu_ms"] / o["ms"], 1)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -540,6 +599,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "cpu_torch": extra_cpu,
+        "cpu_ops": cpu_ops,
         "ops": ops,
         "device": torch.cuda.get_device_name(0),
     }
