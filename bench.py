@@ -481,10 +481,15 @@ def cpu_ops_baseline(oracle):
         ms *= bsz * heads * seq / rows
         out.append(("attention_f16", [bsz, heads, seq, 128], ms,
                     f"{rows} evenly spaced rows of one head, scaled to {bsz * heads * seq} rows"
-                    + (", causal" if causal else "")))
+                    + (", causal" if causal else ""), causal))
         del q, k, v
-    return [{"op": n, "shape": sh, "cpu_ms": round(ms, 3), "sample": smp, "cores": 1}
-            for n, sh, ms, smp in out]
+    entries = []
+    for n, sh, ms, smp, *causal in out:
+        e = {"op": n, "shape": sh, "cpu_ms": round(ms, 3), "sample": smp, "cores": 1}
+        if causal:
+            e["causal"] = causal[0]
+        entries.append(e)
+    return entries
 
 
 def torch_cpu_baseline(torch, budget_s: float):
@@ -582,7 +587,8 @@ def main():
         # GPU / CPU-oracle ratio on the matching op entries
         for c in cpu_ops:
             for o in ops:
-                if o["op"] == c["op"] and o["shape"] == c["shape"] and o.get("ms"):
+                if (o["op"] == c["op"] and o["shape"] == c["shape"] and o.get("ms")
+                        and o.get("causal") == c.get("causal")):
                     o["cpu_oracle_ms"] = c["cpu_ms"]
                     o["speedup_vs_cpu_oracle"] = round(c["cpu_ms"] / o["ms"], 1)
 
