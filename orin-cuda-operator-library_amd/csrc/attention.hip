@@ -442,7 +442,10 @@ __global__ __launch_bounds__(kThreads) void attention_mfma_kernel(
 
 // out[row][d] = sum_s 2^(m_s - m) O_s[row][d] / sum_s 2^(m_s - m) l_s, with
 // m = max_s m_s, over the splits in order (deterministic). One thread per
-// row and 4 consecutive dims (d0 < D).
+// row and 4 consecutive dims (d0 < D); kVec: D % 4 == 0 and a 16-byte
+// aligned output, so the 4 dims move as one float4 (the partials sit in
+// the 256-byte aligned workspace).
+template <bool kVec>
 __global__ __launch_bounds__(256) void attention_combine_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     float* __restrict__ out, long long rows, int D, int splits) {
@@ -458,14 +461,25 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(
     const float w = opl::fast_exp2(part_ml[(sp * rows + row) * 2] - m);
     l += w * part_ml[(sp * rows + row) * 2 + 1];
     const float* o = part_o + (sp * rows + row) * D + d0;
+    if constexpr (kVec) {
+      const float4v v = *reinterpret_cast<const float4v*>(o);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (d0 + r < D) acc[r] += w * o[r];
+      for (int r = 0; r < 4; ++r) acc[r] += w * v[r];
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (d0 + r < D) acc[r] += w * o[r];
+    }
   }
   const float inv = 1.0f / l;
+  if constexpr (kVec) {
+    const float4v v = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+    *reinterpret_cast<float4v*>(out + row * D + d0) = v;
+  } else {
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    if (d0 + r < D) out[row * D + d0 + r] = acc[r] * inv;
+    for (int r = 0; r < 4; ++r)
+      if (d0 + r < D) out[row * D + d0 + r] = acc[r] * inv;
+  }
 }
 
 // Register-staged kernel (one workgroup per CU): small grids deal each
@@ -522,9 +536,13 @@ hipError_t launch_attention(const T* q, const T* k, const T* v, float* out, int 
   if (splits > 1) {
     const long long rows = static_cast<long long>(bh) * s;
     const long long threads = rows * ((d + 3) / 4);
-    attention_combine_kernel<<<dim3(static_cast<unsigned>((threads + 255) / 256)),
-                               dim3(256), 0, stream>>>(part_o, part_ml, out, rows, d,
-                                                        splits);
+    const dim3 cgrid(static_cast<unsigned>((threads + 255) / 256));
+    if (d % 4 == 0 && opl::aligned16(out))
+      attention_combine_kernel<true><<<cgrid, dim3(256), 0, stream>>>(
+          part_o, part_ml, out, rows, d, splits);
+    else
+      attention_combine_kernel<false><<<cgrid, dim3(256), 0, stream>>>(
+          part_o, part_ml, out, rows, d, splits);
   }
   return hipGetLastError();
 }
