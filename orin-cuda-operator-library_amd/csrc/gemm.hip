@@ -819,22 +819,28 @@ void skinny_kernel(
 // block of B into a 16 x 16 block of C, where the vector-ALU kernel spends
 // one dot product per (m, column pair) and becomes ALU-bound as M grows.
 // B is never transposed: the MFMA only needs A and B to agree on which k
-// fills each of its k slots, so lane (g, c) (g = lane / 16, c = lane % 16)
-// loads 16-byte chunks of its R rows (k slots R*g .. R*g+R-1) at columns
-// P*c .. P*c+P-1, and MFMA j takes column j of every lane's chunk: tile
-// column c of MFMA j is matrix column P*c + j, so P MFMAs cover the
-// workgroup's 16 P columns. Each lane reads its A operand values straight
-// from global memory (L2-resident) with its B loads, so nothing waits on a
-// staging barrier. Splits, the workgroup shape and the partial sums are
-// those of skinny_kernel.
+// fills each of its k slots. K is walked in blocks of 16 rows; lane (g, c)
+// (g = lane / 16, c = lane % 16) owns rows 4g .. 4g+3 of each block:
+//   * it loads a 16-byte chunk (columns P*c .. P*c+P-1) of each of those
+//     rows, and MFMA j takes column j of every lane's chunk, so tile column
+//     c of MFMA j is matrix column P*c + j and P MFMAs cover the
+//     workgroup's 16 P columns;
+//   * its A operand values A[c][4g .. 4g+3] are contiguous, one 8-byte
+//     (fp16) or 16-byte (fp32) load straight from global memory (A is
+//     L2-resident), issued with the B loads, so nothing waits on a staging
+//     barrier; rows that are not 4-aligned fall back to element loads;
+//   * fp16 feeds the four rows to one 16x16x16 MFMA (k slots 4g .. 4g+3);
+//     fp32 issues four 16x16x4 MFMAs, the u-th taking row 4g + u in k slot
+//     g.
+// Splits, the workgroup shape and the partial sums are those of
+// skinny_kernel.
 template <typename T>
 struct MfmaCfg;
 template <>
 struct MfmaCfg<_Float16> {
   typedef _Float16 AOp __attribute__((ext_vector_type(4)));
-  static constexpr int kRows = 4;     // B rows per lane per k block
-  static constexpr int kK = 16;       // k per MFMA = rows per k block
-  static constexpr int kBatch = 4;    // k blocks in flight per wavefront
+  typedef _Float16 AVec __attribute__((ext_vector_type(4)));
+  static constexpr int kBatch = 4;    // 16-row k blocks in flight per wavefront
   __device__ static floatx4v mma(AOp a, AOp b, floatx4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
@@ -842,25 +848,30 @@ struct MfmaCfg<_Float16> {
 template <>
 struct MfmaCfg<float> {
   typedef float AOp;
-  static constexpr int kRows = 1;
-  static constexpr int kK = 4;
-  static constexpr int kBatch = 16;
+  typedef float AVec __attribute__((ext_vector_type(4)));
+  static constexpr int kBatch = 4;
   __device__ static floatx4v mma(AOp a, AOp b, floatx4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
 };
 
-template <typename T>
+// Rows of a k block that one lane owns (and the MFMA k slots they fill).
+constexpr int kLaneRows = 4;
+constexpr int kKBlock = 4 * kLaneRows;  // 16
+
+// kVecA: K % 4 == 0 and A aligned to 4 elements, so each lane's four A
+// values of a block are one aligned vector, wholly inside or outside k_end.
+template <typename T, bool kVecA>
 __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
     const T* __restrict__ A, const T* __restrict__ B, float* __restrict__ out,
     int m_rows, int n, int k, int chunk) {
   using MC = MfmaCfg<T>;
   using Vec = typename RowChunk<T>::Vec;  // one 16-byte chunk of a B row
-  using AOp = typename MC::AOp;
+  using AVec = typename MC::AVec;
   constexpr int P = Cfg<T>::kPerLane;     // columns per lane
   constexpr int BN = Cfg<T>::kBlockN;     // 16 * P
-  constexpr int R = MC::kRows;
-  constexpr int KB = MC::kK;
+  constexpr int R = kLaneRows;
+  constexpr int KB = kKBlock;
   constexpr int kBatch = MC::kBatch;
   __shared__ float red[kWaves * opl::kWaveSize * P * 4];
 
@@ -878,25 +889,37 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
   const int blocks = (k_end - k0 + KB - 1) / KB;
 
   // k block b, lane group g: k rows k0 + KB b + R g + q (q < R). B: a
-  // 16-byte chunk of each row; A operand: A[c][row] (read from L2, every
-  // workgroup of the split reads the same A). Rows past k_end read valid
-  // memory and are zeroed, as are A rows past m_rows.
-  auto load_block = [&](int b, Vec (&v)[R], AOp& a) {
+  // 16-byte chunk of each row; A: A[c][row] (read from L2, every workgroup
+  // of the split reads the same A). Rows past k_end read valid memory and
+  // are zeroed, as are A rows past m_rows.
+  auto load_block = [&](int b, Vec (&v)[R], AVec& a) {
+    const int r0 = k0 + KB * b + R * g;
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      const int r = k0 + KB * b + R * g + q;
+      const int r = r0 + q;
       const bool in = r < k_end;
       const int rc = in ? r : k_end - 1;
       Vec x = *reinterpret_cast<const Vec*>(B + static_cast<std::size_t>(rc) * n + col);
 #pragma unroll
       for (int j = 0; j < P; ++j) x[j] = in ? x[j] : T(0);
       v[q] = x;
-      const bool a_in = in && a_row;
-      const T av = A[a_in ? static_cast<std::size_t>(c) * k + r : 0];
-      if constexpr (R == 1)
-        a = a_in ? av : T(0);
-      else
+    }
+    if constexpr (kVecA) {
+      // r0 % 4 == 0 and k_end % 4 == 0: rows r0 .. r0+3 are all in or all
+      // out. Out-of-range lanes read A[0 .. 3] (k >= 4) and zero it.
+      const bool a_in = r0 < k_end && a_row;
+      AVec x = *reinterpret_cast<const AVec*>(
+          A + (a_in ? static_cast<std::size_t>(c) * k + r0 : 0));
+#pragma unroll
+      for (int q = 0; q < R; ++q) a[q] = a_in ? x[q] : T(0);
+    } else {
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        const int r = r0 + q;
+        const bool a_in = r < k_end && a_row;
+        const T av = A[a_in ? static_cast<std::size_t>(c) * k + r : 0];
         a[q] = a_in ? av : T(0);
+      }
     }
   };
 
@@ -907,7 +930,7 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
     for (int e = 0; e < 4; ++e) acc[j][e] = 0.0f;
 
   Vec v[kBatch][R];
-  AOp a[kBatch];
+  AVec a[kBatch];
   for (int b0 = wave; b0 < blocks; b0 += kWaves * kBatch) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -919,14 +942,15 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
       if (b0 + kWaves * u < blocks) {  // wave-uniform
 #pragma unroll
         for (int j = 0; j < P; ++j) {
-          AOp bop;
-          if constexpr (R == 4) {
+          if constexpr (sizeof(T) == 2) {
+            typename MC::AOp bop;
 #pragma unroll
             for (int q = 0; q < R; ++q) bop[q] = v[u][q][j];
+            acc[j] = MC::mma(a[u], bop, acc[j]);
           } else {
-            bop = v[u][0][j];
+#pragma unroll
+            for (int q = 0; q < R; ++q) acc[j] = MC::mma(a[u][q], v[u][q][j], acc[j]);
           }
-          acc[j] = MC::mma(a[u], bop, acc[j]);
         }
       }
     }
@@ -1015,9 +1039,15 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k,
     dst = static_cast<float*>(ws);
   }
   const dim3 grid(static_cast<unsigned>(blocks_n), static_cast<unsigned>(splits));
-  if (m >= C::kMfmaMinM)
-    skinny_mfma_kernel<T><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k, chunk);
-  else if (m == 1) launch_m<T, 1>(a, b, dst, m, n, k, chunk, grid, stream);
+  if (m >= C::kMfmaMinM) {
+    const bool vec_a =
+        k % kLaneRows == 0 &&
+        reinterpret_cast<std::uintptr_t>(a) % (kLaneRows * sizeof(T)) == 0;
+    if (vec_a)
+      skinny_mfma_kernel<T, true><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k, chunk);
+    else
+      skinny_mfma_kernel<T, false><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k, chunk);
+  } else if (m == 1) launch_m<T, 1>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 2) launch_m<T, 2>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 4) launch_m<T, 4>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 8) launch_m<T, 8>(a, b, dst, m, n, k, chunk, grid, stream);

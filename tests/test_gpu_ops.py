@@ -24,7 +24,7 @@ import torch
 
 import oracle
 import pins
-from gpu_util import HipOps
+from gpu_util import HipOps, check, empty, ptr, stream_handle, to_device
 
 pytestmark = pytest.mark.gpu
 
@@ -270,6 +270,32 @@ def test_gemm_skinny(hip, mnk, dtype):
         ref = oracle.gemm(a, b)
         assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
         assert np.all(np.abs(y - ref) <= 1e-3 + 1e-3 * np.abs(ref))
+
+
+@pytest.mark.parametrize("m", [6, 12, 16])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_gemm_skinny_unaligned_a(hip, m, dtype):
+    """K % 4 == 0 but A off its 4-element alignment (B aligned, so the
+    skinny path still applies): the matrix-core kernel's element-wise A
+    loads instead of the vector ones."""
+    n, k = 640, 1024
+    a = oracle.uniform(660 + m, (m, k))
+    b = oracle.uniform(661, (k, n))
+    if dtype == "f16":
+        a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        fn, ref = hip.lib.operatorlib_gemm_f16, oracle.gemm(oracle.from_f16_bits(a),
+                                                             oracle.from_f16_bits(b))
+    else:
+        fn, ref = hip.lib.operatorlib_gemm_f32, oracle.gemm(a, b)
+    da, db = to_device(a, 1), to_device(b)
+    out = empty((m, n))
+    check(fn(ptr(da), ptr(db), ptr(out), m, n, k, stream_handle()), "gemm")
+    torch.cuda.synchronize()
+    y = out.cpu().numpy().astype(np.float64)
+    if dtype == "f16":
+        assert np.max(np.abs(y - ref)) <= 2e-3
+    else:
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
 
 
 def test_gemm_skinny_deterministic(hip):
