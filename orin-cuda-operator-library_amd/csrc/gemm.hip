@@ -820,7 +820,9 @@ void skinny_kernel(
 // one dot product per (m, column pair) and becomes ALU-bound as M grows.
 // B is never transposed: the MFMA only needs A and B to agree on which k
 // fills each of its k slots. K is walked in blocks of 16 rows; lane (g, c)
-// (g = lane / 16, c = lane % 16) owns rows 4g .. 4g+3 of each block:
+// (g = lane / 16, c = lane % 16) owns rows 4g .. 4g+3 of each block (fp32
+// with unaligned A: blocks of 4 rows, row g each, 16 blocks in flight, as
+// the element loads gain nothing from the grouping):
 //   * it loads a 16-byte chunk (columns P*c .. P*c+P-1) of each of those
 //     rows, and MFMA j takes column j of every lane's chunk, so tile column
 //     c of MFMA j is matrix column P*c + j and P MFMAs cover the
@@ -857,7 +859,6 @@ struct MfmaCfg<float> {
 
 // Rows of a k block that one lane owns (and the MFMA k slots they fill).
 constexpr int kLaneRows = 4;
-constexpr int kKBlock = 4 * kLaneRows;  // 16
 
 // kVecA: K % 4 == 0 and A aligned to 4 elements, so each lane's four A
 // values of a block are one aligned vector, wholly inside or outside k_end.
@@ -867,12 +868,17 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
     int m_rows, int n, int k, int chunk) {
   using MC = MfmaCfg<T>;
   using Vec = typename RowChunk<T>::Vec;  // one 16-byte chunk of a B row
-  using AVec = typename MC::AVec;
   constexpr int P = Cfg<T>::kPerLane;     // columns per lane
   constexpr int BN = Cfg<T>::kBlockN;     // 16 * P
-  constexpr int R = kLaneRows;
-  constexpr int KB = kKBlock;
-  constexpr int kBatch = MC::kBatch;
+  // Rows per lane and k block: 4, or 1 for fp32 without vector A loads.
+  constexpr int R = sizeof(T) == 4 && !kVecA ? 1 : kLaneRows;
+  constexpr int KB = 4 * R;  // rows per k block
+  constexpr int kBatch = R == 1 ? 16 : MC::kBatch;
+  using AVec = typename std::conditional<R == 1, T, typename MC::AVec>::type;
+  // k slot q of a lane's A values
+  auto a_at = [](const AVec& a, int q) -> T {
+    if constexpr (R == 1) return a; else return a[q];
+  };
   __shared__ float red[kWaves * opl::kWaveSize * P * 4];
 
   const int n0 = blockIdx.x * BN;
@@ -903,6 +909,15 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
 #pragma unroll
       for (int j = 0; j < P; ++j) x[j] = in ? x[j] : T(0);
       v[q] = x;
+      if constexpr (!kVecA) {
+        // element loads, each issued beside its B row's load
+        const bool a_in = in && a_row;
+        const T av = A[a_in ? static_cast<std::size_t>(c) * k + r : 0];
+        if constexpr (R == 1)
+          a = a_in ? av : T(0);
+        else
+          a[q] = a_in ? av : T(0);
+      }
     }
     if constexpr (kVecA) {
       // r0 % 4 == 0 and k_end % 4 == 0: rows r0 .. r0+3 are all in or all
@@ -912,14 +927,6 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
           A + (a_in ? static_cast<std::size_t>(c) * k + r0 : 0));
 #pragma unroll
       for (int q = 0; q < R; ++q) a[q] = a_in ? x[q] : T(0);
-    } else {
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int r = r0 + q;
-        const bool a_in = r < k_end && a_row;
-        const T av = A[a_in ? static_cast<std::size_t>(c) * k + r : 0];
-        a[q] = a_in ? av : T(0);
-      }
     }
   };
 
@@ -949,7 +956,7 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
             acc[j] = MC::mma(a[u], bop, acc[j]);
           } else {
 #pragma unroll
-            for (int q = 0; q < R; ++q) acc[j] = MC::mma(a[u][q], v[u][q][j], acc[j]);
+            for (int q = 0; q < R; ++q) acc[j] = MC::mma(a_at(a[u], q), v[u][q][j], acc[j]);
           }
         }
       }
