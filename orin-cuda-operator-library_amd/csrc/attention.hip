@@ -587,6 +587,13 @@ constexpr int kXcds = 8;
 // 85.0, causal 61.0 vs 63.6; B4 H32 S8192 causal 2238 vs 2408.
 constexpr long long kSplitKeysBelow = 256;
 constexpr long long kSplitKeysBelowCausal = 512;
+// Grids of at most this many 128-row query blocks run 64-row blocks (two
+// groups of two wavefronts), so that twice as many CUs share the work.
+// Measured on MI355X (us, 128- vs 64-row blocks, keys split in both): B1
+// H12 S1024 20.6 vs 17.6 (causal 20.6 vs 17.5); B1 H8 S2048 34.0 vs 30.0;
+// B1 H4 S512 causal 13.2 vs 10.7; past 128 blocks the 64-row grid needs
+// more than one workgroup per CU: B1 H12 S2048 (192) 35.5 vs 55.3.
+constexpr long long kHalfRowsUpTo = 128;
 // Headroom (log2 units) the running row max may lag the true max by.
 constexpr float kLazyLog2 = 8.0f;
 
@@ -596,7 +603,6 @@ struct Layout {
   static constexpr int kChunks = kRowBytes / 16;
   static constexpr int kTile = kKeys * kRowBytes;  // one K or V tile
   static constexpr int kStage = 2 * kTile;
-  static constexpr int kCopies = kTile / 16 / kThreads;
   static constexpr int kSteps = D / 16;  // QK^T k-steps
   static constexpr int kDTiles = D / 32;
   __device__ static int swizzle_k(int row) {
@@ -607,14 +613,20 @@ struct Layout {
   }
 };
 
-// kGroups = 2 (small grids): two groups of 4 wavefronts share the
-// workgroup's 128 query rows and split its key tiles, group 0 the first
-// half and group 1 the rest, each with its own K/V stages; at the end group
-// 1 hands its (O, max, sum) to group 0 through LDS, which merges them. A
-// workgroup then fills a CU (8 wavefronts, 128 KiB of LDS) and each
-// wavefront walks half the keys.
-template <int D, int kGroups>
-__global__ __launch_bounds__(kThreads * kGroups) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// kGroups = 2 (small grids): two groups of kW wavefronts share the
+// workgroup's query rows and split its key tiles, group 0 the first half
+// and group 1 the rest, each with its own K/V stages; at the end group 1
+// hands its (O, max, sum) to group 0 through LDS, which merges them. A
+// workgroup then holds 128 KiB of LDS (a CU) and each wavefront walks half
+// the keys.
+// kW = wavefronts per group, 32 query rows each: 4 (128-row blocks), or 2
+// (64-row blocks) for the smallest grids, whose 128-row blocks would leave
+// CUs idle: twice the workgroups, one wavefront per SIMD.
+// The 128 KiB of LDS of a D = 128 workgroup fill a CU: with kW = 2 that is
+// one wavefront per SIMD, otherwise two.
+template <int D, int kGroups, int kW>
+__global__ __launch_bounds__(kW * opl::kWaveSize * kGroups)
+__attribute__((amdgpu_waves_per_eu(D == 128 && kW == 2 ? 1 : 2, 2)))
 void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
                               const _Float16* __restrict__ K,
                               const _Float16* __restrict__ V,
@@ -622,6 +634,10 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
                               float score_scale_log2) {
   using L = Layout<D>;
   static_assert(kGroups == 1 || kGroups == 2, "one or two key groups");
+  static_assert(kW == 2 || kW == 4, "2 or 4 wavefronts per group");
+  constexpr int kRows = kW * kRowsPerWave;  // query rows per workgroup
+  // 16-byte copies per lane and tile: the group's lanes share each tile
+  constexpr int kCopies = L::kTile / 16 / (kW * opl::kWaveSize);
   __shared__ __attribute__((aligned(1024))) unsigned char stage0[kGroups * L::kStage];
   __shared__ __attribute__((aligned(1024))) unsigned char stage1[kGroups * L::kStage];
 
@@ -631,7 +647,7 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   // [x * per_xcd, (x + 1) * per_xcd), so the workgroups resident on one XCD
   // at a time belong to one or two heads and share that head's K/V tiles
   // in the XCD's L2 instead of streaming them from HBM per query block.
-  const int q_blocks = S / kBlockRows;
+  const int q_blocks = S / kRows;
   const int total = q_blocks * BH;
   const int per_xcd = (total + kXcds - 1) / kXcds;
   const int w = static_cast<int>(blockIdx.x % kXcds) * per_xcd +
@@ -639,13 +655,13 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   if (w >= total) return;  // padding of the grid to a multiple of 8
   const int bh = w / q_blocks;
   const int qb = q_blocks - 1 - w % q_blocks;
-  const int q0 = qb * kBlockRows;
+  const int q0 = qb * kRows;
   const int lane = threadIdx.x % opl::kWaveSize;
   // (Kept as a vector value: declaring it wave-uniform turns the causal
   // tests into scalar branches and measured ~8% slower.)
-  const int wave = (threadIdx.x / opl::kWaveSize) % kWaves;
+  const int wave = (threadIdx.x / opl::kWaveSize) % kW;
   const int group = kGroups == 1 ? 0 : __builtin_amdgcn_readfirstlane(
-                                           threadIdx.x / opl::kWaveSize / kWaves);
+                                           threadIdx.x / opl::kWaveSize / kW);
   unsigned char* const st0 = stage0 + group * L::kStage;
   unsigned char* const st1 = stage1 + group * L::kStage;
   const int half = lane / 32;
@@ -664,10 +680,10 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
         qh + static_cast<std::size_t>(my_row) * D + 16 * c + 8 * half);
 
   // DMA: element offset of the chunk this lane copies, per copy.
-  int k_src[L::kCopies], v_src[L::kCopies];
+  int k_src[kCopies], v_src[kCopies];
 #pragma unroll
-  for (int j = 0; j < L::kCopies; ++j) {
-    const int slot = (wave * L::kCopies + j) * 64 + lane;
+  for (int j = 0; j < kCopies; ++j) {
+    const int slot = (wave * kCopies + j) * 64 + lane;
     const int row = slot / L::kChunks;
     const int phys = slot % L::kChunks;
     k_src[j] = row * D + 8 * (phys ^ L::swizzle_k(row));
@@ -679,7 +695,7 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   // vector address arithmetic.
   const unsigned head_bytes = static_cast<unsigned>(S) * D * 2u;
 #pragma unroll
-  for (int j = 0; j < L::kCopies; ++j) {
+  for (int j = 0; j < kCopies; ++j) {
     k_src[j] *= 2;  // elements -> bytes
     v_src[j] *= 2;
   }
@@ -691,12 +707,12 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     // < head_bytes < 2^32: unsigned, so a head above 2 GiB cannot overflow
     const unsigned tile_bytes = static_cast<unsigned>(key0) * D * 2u;
 #pragma unroll
-    for (int j = 0; j < L::kCopies; ++j)
-      opl::buffer_copy16_lds(kh, head_bytes, st + (wave_s * L::kCopies + j) * 1024,
+    for (int j = 0; j < kCopies; ++j)
+      opl::buffer_copy16_lds(kh, head_bytes, st + (wave_s * kCopies + j) * 1024,
                         k_src[j], tile_bytes);
 #pragma unroll
-    for (int j = 0; j < L::kCopies; ++j)
-      opl::buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave_s * L::kCopies + j) * 1024,
+    for (int j = 0; j < kCopies; ++j)
+      opl::buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave_s * kCopies + j) * 1024,
                         v_src[j], tile_bytes);
   };
   // K^T-operand rows are l32 (+32 for the second 32-key block, an immediate).
@@ -728,7 +744,7 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   // visible score.
   float move_above = -INFINITY;
   const float inv_scale = 1.0f / score_scale_log2;
-  const int visible_end = causal ? min(S, q0 + kBlockRows) : S;
+  const int visible_end = causal ? min(S, q0 + kRows) : S;
   const int tiles = (visible_end + kKeys - 1) / kKeys;
   // This group's tiles [t_begin, t_begin + t_count); both groups run
   // `iters` iterations so that they meet at every barrier.
@@ -885,7 +901,7 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     float* xo = reinterpret_cast<float*>(stage0);
     float* xs = reinterpret_cast<float*>(stage1);
     const int slot = wave * opl::kWaveSize + lane;
-    constexpr int kSlots = kWaves * opl::kWaveSize;
+    constexpr int kSlots = kW * opl::kWaveSize;
     static_assert(L::kDTiles * 16 * kSlots * 4 <= 2 * L::kStage, "O exchange fits stage0");
     if (group == 1) {
 #pragma unroll
@@ -960,27 +976,36 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
     if (f16_dma_ok(q, k, v, out, sequence, head_dim)) {
       const float scale =
           1.4426950408889634f / sqrtf(static_cast<float>(head_dim));
-      // a multiple of 8 workgroups, one contiguous range of work per XCD
-      const long long padded = (blocks + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
-      const dim3 grid(static_cast<unsigned>(padded));
       // Grids too small to fill the CUs split each query block's keys
-      // between two groups of wavefronts in the workgroup.
-      const bool split =
+      // between two groups of wavefronts in the workgroup; the smallest
+      // also halve the query block.
+      const bool half_rows = blocks <= dma::kHalfRowsUpTo;
+      const bool split = half_rows ||
           blocks < (causal ? dma::kSplitKeysBelowCausal : dma::kSplitKeysBelow);
-      const dim3 block(split ? 2 * kThreads : kThreads);
+      const long long wgs = half_rows ? 2 * blocks : blocks;
+      // a multiple of 8 workgroups, one contiguous range of work per XCD
+      const long long padded = (wgs + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
+      const dim3 grid(static_cast<unsigned>(padded));
+      const dim3 block(half_rows || !split ? kThreads : 2 * kThreads);
       if (head_dim == 128) {
-        if (split)
-          dma::attention_f16_dma_kernel<128, 2><<<grid, block, 0, stream>>>(
+        if (half_rows)
+          dma::attention_f16_dma_kernel<128, 2, 2><<<grid, block, 0, stream>>>(
+              q, k, v, out, bh, sequence, c, scale);
+        else if (split)
+          dma::attention_f16_dma_kernel<128, 2, 4><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else
-          dma::attention_f16_dma_kernel<128, 1><<<grid, block, 0, stream>>>(
+          dma::attention_f16_dma_kernel<128, 1, 4><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
       } else {
-        if (split)
-          dma::attention_f16_dma_kernel<64, 2><<<grid, block, 0, stream>>>(
+        if (half_rows)
+          dma::attention_f16_dma_kernel<64, 2, 2><<<grid, block, 0, stream>>>(
+              q, k, v, out, bh, sequence, c, scale);
+        else if (split)
+          dma::attention_f16_dma_kernel<64, 2, 4><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else
-          dma::attention_f16_dma_kernel<64, 1><<<grid, block, 0, stream>>>(
+          dma::attention_f16_dma_kernel<64, 1, 4><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
       }
       return hipGetLastError();
