@@ -31,11 +31,14 @@ def _inputs(device):
         "x": mk(1_000_003),
         "sm": mk(300, 1003) * 3,
         "tr": mk(520, 260),
+        "tr2": mk(1030, 1031),  # 16-byte accesses at 4-byte alignment
         "rn": mk(257, 4096),
         "w": mk(4096).abs() + 0.5,
         "a": mk(300, 640), "b": mk(640, 512),
         "ah": mk(1000, 1000, dtype=torch.float16), "bh": mk(1000, 1000, dtype=torch.float16),
         "a1": mk(1, 4096, dtype=torch.float16), "b1": mk(4096, 4096, dtype=torch.float16),
+        "a16": mk(16, 4096, dtype=torch.float16),
+        "a12": mk(12, 1024), "b32": mk(1024, 2048),
         "q": mk(1, 4, 256, 128, dtype=torch.float16),
         "k": mk(1, 4, 256, 128, dtype=torch.float16),
         "v": mk(1, 4, 256, 128, dtype=torch.float16),
@@ -47,12 +50,15 @@ def _all_ops(ops, t):
         ops.reduce_sum(t["x"]),
         ops.softmax(t["sm"]),
         ops.transpose(t["tr"]),
+        ops.transpose(t["tr2"]),
         ops.rmsnorm(t["rn"], t["w"], 1e-6),
         ops.softmax(t["sm"].half()),
         ops.rmsnorm(t["rn"].half(), t["w"].half(), 1e-6),
         ops.gemm(t["a"], t["b"]),
         ops.gemm(t["ah"], t["bh"]),      # zero-padded workspace path
         ops.gemm(t["a1"], t["b1"]),      # skinny path with K splits
+        ops.gemm(t["a16"], t["b1"]),     # matrix-core skinny kernel, vector A
+        ops.gemm(t["a12"], t["b32"]),    # same, fp32
         ops.attention(t["q"], t["k"], t["v"], True),
         # fp32, 8 query blocks: keys split over workgroups, partials in the
         # workspace, then the combine kernel
