@@ -40,6 +40,12 @@ namespace {
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / opl::kWaveSize;
 constexpr int kUnroll = 4;
+// Pass-1 grid cap: one workgroup per CU, each walking several chunks.
+// Measured on MI355X, n = 2^24, inputs cycling through 1 GiB (us, grid cap
+// 256 / 512 / 1024): 12.88 / 13.25 / 13.76 with 4 loads in flight per
+// thread; 8 or 16 in flight were no faster (13.35-14.14).
+constexpr int kGridBlocks = 256;
+static_assert(kGridBlocks <= opl::kReduceMaxBlocks, "partials fit the scratch");
 constexpr int kCombineThreads = 256;
 
 typedef float float4v __attribute__((ext_vector_type(4)));
@@ -126,7 +132,7 @@ extern "C" int operatorlib_reduce_sum_f32(const float* input, float* output,
   const std::size_t wanted = std::max<std::size_t>(
       1, (nvec + chunk - 1) / chunk);
   const int blocks = static_cast<int>(
-      std::min<std::size_t>(wanted, opl::kReduceMaxBlocks));
+      std::min<std::size_t>(wanted, kGridBlocks));
   double* partials = nullptr;
   if (blocks > 1) {
     const hipError_t status = opl::reduce_partials_for_stream(stream, &partials);
