@@ -75,8 +75,8 @@ def parse_args():
 
 # --------------------------------------------------------------------- helpers
 
-PROFILE_OPS = {"copy", "reduce", "softmax", "rmsnorm", "transpose", "gemm_f32", "gemm_f16",
-               "attention_f16"}
+PROFILE_OPS = {"copy", "reduce", "softmax", "rmsnorm", "transpose", "transpose_ragged",
+               "gemm_f32", "gemm_f16", "attention_f16"}
 
 
 def profile_only(torch, lib, oracle, ptr, op: str, launches: int) -> None:
@@ -101,10 +101,11 @@ def profile_only(torch, lib, oracle, ptr, op: str, launches: int) -> None:
         w = torch.rand(4096, device=dev, generator=gen) + 0.5
         y = torch.empty_like(x)
         f = lambda: lib.operatorlib_rmsnorm_f32(ptr(x), ptr(w), ptr(y), 2048, 4096, 1e-6, stream)
-    elif op == "transpose":
-        x = torch.rand(4096, 4096, device=dev, generator=gen)
-        y = torch.empty_like(x)
-        f = lambda: lib.operatorlib_transpose_f32(ptr(x), ptr(y), 4096, 4096, stream)
+    elif op in ("transpose", "transpose_ragged"):
+        rows, cols = (4096, 4096) if op == "transpose" else (4095, 4097)
+        x = torch.rand(rows, cols, device=dev, generator=gen)
+        y = torch.empty(cols, rows, device=dev)
+        f = lambda: lib.operatorlib_transpose_f32(ptr(x), ptr(y), rows, cols, stream)
     elif op in ("gemm_f32", "gemm_f16"):
         n = 4096 if op == "gemm_f32" else 8192
         a = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
