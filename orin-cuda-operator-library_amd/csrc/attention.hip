@@ -594,6 +594,17 @@ constexpr long long kSplitKeysBelowCausal = 512;
 // B1 H4 S512 causal 13.2 vs 10.7; past 128 blocks the 64-row grid needs
 // more than one workgroup per CU: B1 H12 S2048 (192) 35.5 vs 55.3.
 constexpr long long kHalfRowsUpTo = 128;
+// D = 64 workgroups hold 64 KiB of LDS (two per CU), so 64-row blocks pay
+// off on larger grids. Measured (us, 128- vs 64-row blocks): B1 H32 S1024
+// (256 blocks) 17.4 vs 15.2; B1 H12 S4096 (384) 75.9 vs 72.5, causal 48.5
+// vs 47.5; B1 H16 S4096 (512) 84.7 vs 90.5, causal (128-row keys unsplit)
+// 73.1 vs 52.9. These limits cover every grid that would split keys on
+// 128-row blocks, so D = 64 never runs that instance.
+constexpr long long kHalfRowsUpToD64 = 384;
+constexpr long long kHalfRowsUpToD64Causal = 512;
+static_assert(kHalfRowsUpToD64 >= kSplitKeysBelow - 1 &&
+                  kHalfRowsUpToD64Causal >= kSplitKeysBelowCausal - 1,
+              "every D = 64 grid that splits keys runs 64-row blocks");
 // Headroom (log2 units) the running row max may lag the true max by.
 constexpr float kLazyLog2 = 8.0f;
 
@@ -979,7 +990,10 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
       // Grids too small to fill the CUs split each query block's keys
       // between two groups of wavefronts in the workgroup; the smallest
       // also halve the query block.
-      const bool half_rows = blocks <= dma::kHalfRowsUpTo;
+      const long long half_up_to =
+          head_dim == 128 ? dma::kHalfRowsUpTo
+                          : (causal ? dma::kHalfRowsUpToD64Causal : dma::kHalfRowsUpToD64);
+      const bool half_rows = blocks <= half_up_to;
       const bool split = half_rows ||
           blocks < (causal ? dma::kSplitKeysBelowCausal : dma::kSplitKeysBelow);
       const long long wgs = half_rows ? 2 * blocks : blocks;
@@ -998,11 +1012,9 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
           dma::attention_f16_dma_kernel<128, 1, 4><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
       } else {
+        // (split implies half_rows at D = 64)
         if (half_rows)
           dma::attention_f16_dma_kernel<64, 2, 2><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
-        else if (split)
-          dma::attention_f16_dma_kernel<64, 2, 4><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else
           dma::attention_f16_dma_kernel<64, 1, 4><<<grid, block, 0, stream>>>(
