@@ -174,3 +174,14 @@ def test_torch_ops_have_no_cpu_kernel():
     operatorlib.load_operatorlib()
     with pytest.raises(NotImplementedError):
         torch.ops.operatorlib.softmax(torch.ones(2, 2))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """The bench measures one GPU; any other --gpus value exits with a
+    message (status 2) before touching a device."""
+    import sys
+    proc = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 2
+    assert "--gpus 2 is not supported" in proc.stdout + proc.stderr
+    assert not proc.stdout.strip().startswith("{")  # no bench line
