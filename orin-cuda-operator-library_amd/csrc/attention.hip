@@ -46,6 +46,7 @@
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
+#include <optional>
 #include <type_traits>
 
 #include "common.hpp"
@@ -508,13 +509,16 @@ hipError_t launch_attention(const T* q, const T* k, const T* v, float* out, int 
   if (splits < 1) splits = 1;
   float* part_o = nullptr;
   float* part_ml = nullptr;
+  // Held until the combine kernel is enqueued (scratch.hpp).
+  std::optional<opl::ScratchLease> lease;
   if (splits > 1) {
     const std::size_t rows = static_cast<std::size_t>(bh) * s;
-    void* ws = nullptr;
-    const hipError_t status = opl::workspace_for_stream(
-        stream, static_cast<std::size_t>(splits) * rows * (d + 2) * sizeof(float), &ws);
+    lease.emplace(stream);
+    opl::Scratch scratch;
+    const hipError_t status = lease->get(
+        static_cast<std::size_t>(splits) * rows * (d + 2) * sizeof(float), &scratch);
     if (status != hipSuccess) return status;
-    part_o = static_cast<float*>(ws);
+    part_o = static_cast<float*>(scratch.data);
     part_ml = part_o + static_cast<std::size_t>(splits) * rows * d;
   }
   const dim3 grid(static_cast<unsigned>(blocks * splits)), block(kThreads);

@@ -47,6 +47,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <optional>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1038,12 +1039,15 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k,
   if (chunk > kMaxChunk) chunk = kMaxChunk;
   splits = (k + chunk - 1) / chunk;
   float* dst = c;
+  // Held until the split sum is enqueued (scratch.hpp).
+  std::optional<opl::ScratchLease> lease;
   if (splits > 1) {
-    void* ws = nullptr;
-    const hipError_t status = opl::workspace_for_stream(
-        stream, static_cast<std::size_t>(splits) * m * n * sizeof(float), &ws);
+    lease.emplace(stream);
+    opl::Scratch scratch;
+    const hipError_t status = lease->get(
+        static_cast<std::size_t>(splits) * m * n * sizeof(float), &scratch);
     if (status != hipSuccess) return status;
-    dst = static_cast<float*>(ws);
+    dst = static_cast<float*>(scratch.data);
   }
   const dim3 grid(static_cast<unsigned>(blocks_n), static_cast<unsigned>(splits));
   if (m >= C::kMfmaMinM) {
@@ -1157,10 +1161,12 @@ struct PaddedOperands {
   int ldb;  // row stride of B
 };
 
-// Pads A to [m, kp] and/or B to [kp, np] in the stream's workspace as needed.
+// Pads A to [m, kp] and/or B to [kp, np] in library scratch as needed. The
+// caller keeps `lease` until the product that reads the copies is enqueued.
 template <typename T>
 hipError_t pad_operands(const T* a, const T* b, int m, int n, int k, int k_mult,
-                        int n_mult, hipStream_t stream, PaddedOperands* out) {
+                        int n_mult, hipStream_t stream, opl::ScratchLease& lease,
+                        PaddedOperands* out) {
   const long long kp = round_up(k, k_mult);
   const long long np = round_up(n, n_mult);
   const bool pad_a = kp != k || !opl::aligned16(a);
@@ -1169,9 +1175,10 @@ hipError_t pad_operands(const T* a, const T* b, int m, int n, int k, int k_mult,
   const std::size_t a_bytes =
       pad_a ? static_cast<std::size_t>(round_up(static_cast<long long>(m) * kp * sizeof(T), 256)) : 0;
   const std::size_t b_bytes = pad_b ? static_cast<std::size_t>(kp * np * sizeof(T)) : 0;
-  void* ws = nullptr;
-  hipError_t status = opl::workspace_for_stream(stream, a_bytes + b_bytes, &ws);
+  opl::Scratch scratch;
+  hipError_t status = lease.get(a_bytes + b_bytes, &scratch);
   if (status != hipSuccess) return status;
+  void* ws = scratch.data;
   T* pa = static_cast<T*>(ws);
   T* pb = reinterpret_cast<T*>(static_cast<unsigned char*>(ws) + a_bytes);
   if (pad_a) launch_pad_copy<T>(a, m, k, pa, m, static_cast<int>(kp), stream);
@@ -1229,8 +1236,9 @@ hipError_t launch_gemm(const T* a, const T* b, float* c, int m, int n, int k,
                          opl::aligned16(b);
   if (vector_ok) return launch_generic_for<T>(true, a, b, c, m, n, k, n, stream);
   if (worth_padding(m, n, k)) {
+    opl::ScratchLease lease(stream);
     PaddedOperands p;
-    const hipError_t status = pad_operands<T>(a, b, m, n, k, E, E, stream, &p);
+    const hipError_t status = pad_operands<T>(a, b, m, n, k, E, E, stream, lease, &p);
     if (status != hipSuccess) return status;
     return launch_generic_for<T>(true, static_cast<const T*>(p.a),
                                  static_cast<const T*>(p.b), c, m, n, p.k, p.ldb, stream);
@@ -1292,9 +1300,10 @@ extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
       opl::aligned16(b))
     return launch_gemm_f16_dma(ha, hb, c, m, n, k, n, stream);
   if (dma_offsets_fit && worth_padding(m, n, k)) {
+    opl::ScratchLease lease(stream);
     PaddedOperands p;
     const hipError_t status =
-        pad_operands<_Float16>(ha, hb, m, n, k, dma::kBK, 8, stream, &p);
+        pad_operands<_Float16>(ha, hb, m, n, k, dma::kBK, 8, stream, lease, &p);
     if (status != hipSuccess) return status;
     return launch_gemm_f16_dma(static_cast<const _Float16*>(p.a),
                                static_cast<const _Float16*>(p.b), c, m, n, p.k,

@@ -9,19 +9,22 @@
 //   * pass 1: 512-thread workgroups stream 16-byte loads, kUnroll in flight
 //     per thread; each float4 is summed in fp32 and accumulated in an fp64
 //     register, so rounding error stays far below the fp32 result ulp even
-//     for ill-conditioned (zero-mean) inputs; a wave64 DPP/swizzle fp64
+//     for ill-conditioned (zero-mean) inputs; a wave64 DPP/permlane fp64
 //     reduction and an 8-slot LDS combine give one fp64 partial per
-//     workgroup, written to library scratch;
+//     workgroup, written to library scratch (scratch.hpp);
 //   * pass 2: one workgroup adds the partials in index order and writes the
 //     fp32 result (stream order makes pass 1's partials visible).
 // Inputs that fit one workgroup skip pass 2. No memset, no float atomics.
 //
 // Why two launches: combining in the same launch needs each workgroup to
-// publish its partial at agent scope. On MI355X that costs either an L2
-// writeback per workgroup (release fence; measured ~300 us for 2048
-// workgroups) or a burst of same-address device atomics (~15 ns each,
-// serialized). The second launch costs ~3 us; measured 14.7 us per 64 MiB
-// call versus 11.5 us for a read-only pass over the same bytes.
+// publish its partial at device scope and count arrivals. With a release
+// fence that costs an L2 writeback per workgroup (~300 us for 2048
+// workgroups); with device-scope stores and one arrival counter the
+// arrivals serialize on the counter's address. Measured on one MI355X,
+// n = 2^24, inputs cycling through 1 GiB (us per call, median of 6 runs of
+// 50 back-to-back calls): pass 1 alone 11.13; pass 1 + combine launch
+// 12.89; one launch with an arrival counter 14.07 (256 workgroups) and
+// 16.61 (512).
 // Algorithmic traffic: 4 * n bytes read, 4 bytes written.
 
 #include <hip/hip_runtime.h>
@@ -45,7 +48,6 @@ constexpr int kUnroll = 4;
 // 256 / 512 / 1024): 12.88 / 13.25 / 13.76 with 4 loads in flight per
 // thread; 8 or 16 in flight were no faster (13.35-14.14).
 constexpr int kGridBlocks = 256;
-static_assert(kGridBlocks <= opl::kReduceMaxBlocks, "partials fit the scratch");
 constexpr int kCombineThreads = 256;
 
 typedef float float4v __attribute__((ext_vector_type(4)));
@@ -133,15 +135,20 @@ extern "C" int operatorlib_reduce_sum_f32(const float* input, float* output,
       1, (nvec + chunk - 1) / chunk);
   const int blocks = static_cast<int>(
       std::min<std::size_t>(wanted, kGridBlocks));
-  double* partials = nullptr;
-  if (blocks > 1) {
-    const hipError_t status = opl::reduce_partials_for_stream(stream, &partials);
-    if (status != hipSuccess) return status;
+  if (blocks == 1) {
+    reduce_partials_kernel<<<1, kThreads, 0, stream>>>(input, output, n, head,
+                                                       nvec, nullptr);
+    return hipGetLastError();
   }
+  // Held until the combine kernel is enqueued (scratch.hpp).
+  opl::ScratchLease lease(stream);
+  opl::Scratch scratch;
+  const hipError_t status = lease.get(sizeof(double) * kGridBlocks, &scratch);
+  if (status != hipSuccess) return status;
+  double* partials = static_cast<double*>(scratch.data);
   reduce_partials_kernel<<<blocks, kThreads, 0, stream>>>(input, output, n,
                                                           head, nvec, partials);
-  if (blocks > 1)
-    reduce_combine_kernel<<<1, kCombineThreads, 0, stream>>>(partials, blocks,
-                                                             output);
+  reduce_combine_kernel<<<1, kCombineThreads, 0, stream>>>(partials, blocks,
+                                                           output);
   return hipGetLastError();
 }

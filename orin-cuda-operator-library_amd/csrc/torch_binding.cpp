@@ -1,12 +1,21 @@
-// torch.ops.operatorlib.* — PyTorch custom-op layer over the operatorlib C++
-// API. Drop-in for the reference's python/operatorlib_binding.cpp: the same
-// schema (:190-197), the same argument checks in the same order and with the
-// same error texts (:13-41 and each op), the same output allocation, and the
-// implementations registered on the CUDA dispatch key (:199-206), which is
-// where PyTorch-ROCm keeps HIP tensors.
+// torch.ops.operatorlib.* over the C ABI (operatorlib/operatorlib_c.h).
 //
-// Each op validates, sets a device guard, allocates its output, and enqueues
-// on the current stream of the input's device. It never copies or syncs.
+// Drop-in for the reference's python/operatorlib_binding.cpp: the same six
+// schema strings (:190-197) registered on the CUDA dispatch key (:199-206),
+// which is where PyTorch-ROCm keeps HIP tensors; the same output shapes and
+// dtypes (0-d reduce, input-shaped softmax / rmsnorm, [cols, rows]
+// transpose, fp32 GEMM and attention outputs); work enqueued on the current
+// stream of the inputs' device, never copied, never synchronized. Error
+// texts contain the substrings the reference's tests assert
+// (python/test_extension.py:124-168): "float32", "contiguous",
+// "positive int32", "2D", "weight length", "a.size(1)", "at most 128", and
+// "<op> launch failed: " for launch errors.
+//
+// Structure: an Operands object checks what every operator requires of its
+// tensors (HIP device memory on one device, dense row-major, one dtype from
+// the operator's set); extent() turns a tensor size into the int the C ABI
+// takes; launch() runs one C ABI call under a device guard on the current
+// stream. Each operator then states only its own shape rules.
 
 #include <ATen/ATen.h>
 #include <ATen/hip/HIPContext.h>
@@ -15,206 +24,220 @@
 
 #include <cmath>
 #include <cstdint>
+#include <initializer_list>
 #include <limits>
+#include <string>
+#include <utility>
+#include <vector>
 
-#include "operatorlib/operators.h"
+#include "operatorlib/operatorlib_c.h"
 
 namespace {
 
-void check_cuda_contiguous(const at::Tensor& tensor, const char* name) {
-  TORCH_CHECK(tensor.is_cuda(), name, " must be a CUDA tensor");
-  TORCH_CHECK(tensor.is_contiguous(), name, " must be contiguous");
+enum DTypes { kFloat32Only, kFloat32OrFloat16 };
+
+const char* dtype_set_text(DTypes set) {
+  return set == kFloat32Only ? "float32" : "float32 or float16";
 }
 
-void check_same_device_dtype(const at::Tensor& first, const at::Tensor& second,
-                             const char* first_name, const char* second_name) {
-  TORCH_CHECK(first.device() == second.device(), first_name, " and ",
-              second_name, " must be on the same CUDA device");
-  TORCH_CHECK(first.scalar_type() == second.scalar_type(), first_name, " and ",
-              second_name, " must have the same dtype");
-}
+class Operands {
+ public:
+  // `named` lists (tensor, argument name); the first tensor sets the device
+  // and dtype the others must share.
+  Operands(const char* op, DTypes allowed,
+           std::initializer_list<std::pair<const at::Tensor*, const char*>> named)
+      : op_(op), list_(named) {
+    const at::Tensor& lead = *list_.front().first;
+    for (const auto& [t, name] : list_) {
+      TORCH_CHECK(t->is_cuda(), op_, ": ", name,
+                  " must live in HIP device memory (a CUDA-key tensor), got ",
+                  t->device());
+      TORCH_CHECK(t->is_contiguous(), op_, ": ", name,
+                  " must be contiguous (dense row-major)");
+      TORCH_CHECK(t->device() == lead.device(), op_, ": ", name, " is on ",
+                  t->device(), " but ", list_.front().second, " is on ", lead.device());
+      TORCH_CHECK(t->scalar_type() == lead.scalar_type(), op_, ": ", name,
+                  " has dtype ", t->scalar_type(), " but ", list_.front().second,
+                  " has dtype ", lead.scalar_type());
+    }
+    const at::ScalarType dt = lead.scalar_type();
+    const bool ok = dt == at::kFloat || (allowed == kFloat32OrFloat16 && dt == at::kHalf);
+    TORCH_CHECK(ok, op_, ": inputs must be ", dtype_set_text(allowed), ", got ", dt);
+    half_ = dt == at::kHalf;
+  }
 
-int checked_positive_int(int64_t value, const char* name) {
-  TORCH_CHECK(value > 0 && value <= std::numeric_limits<int>::max(), name,
-              " must be in the positive int32 range");
+  bool half() const { return half_; }
+  const at::Tensor& lead() const { return *list_.front().first; }
+  const char* op() const { return op_; }
+
+ private:
+  const char* op_;
+  std::vector<std::pair<const at::Tensor*, const char*>> list_;
+  bool half_ = false;
+};
+
+// A size the C ABI takes as int: positive and within int32.
+int extent(const char* op, const char* what, std::int64_t value) {
+  TORCH_CHECK(value > 0 && value <= std::numeric_limits<int>::max(), op, ": ",
+              what, " = ", value, " is not a positive int32");
   return static_cast<int>(value);
 }
 
-void check_launch(hipError_t error, const char* operation) {
-  TORCH_CHECK(error == hipSuccess, operation, " launch failed: ",
-              hipGetErrorString(error));
+void require_rank(const Operands& in, const at::Tensor& t, const char* name,
+                  std::int64_t rank, const char* layout) {
+  TORCH_CHECK(t.dim() == rank, in.op(), ": ", name, " must be ", layout, ", got ",
+              t.dim(), " dimension(s)");
 }
 
-hipStream_t current_stream(const at::Tensor& tensor) {
-  return at::hip::getCurrentHIPStreamMasqueradingAsCUDA(tensor.get_device())
-      .stream();
+// Rows of a tensor read as [rows, size(-1)].
+std::pair<int, int> rows_by_last(const Operands& in, const at::Tensor& t,
+                                 const char* last_name) {
+  TORCH_CHECK(t.dim() >= 1, in.op(), ": ", "input must have at least one dimension");
+  const int last = extent(in.op(), last_name, t.size(-1));
+  const int rows = extent(in.op(), "row count (numel / size(-1))", t.numel() / t.size(-1));
+  return {rows, last};
 }
 
-at::Tensor reduce_sum_hip(const at::Tensor& input) {
-  check_cuda_contiguous(input, "input");
-  TORCH_CHECK(input.scalar_type() == at::kFloat,
-              "reduce_sum supports float32 input only");
-  TORCH_CHECK(input.numel() > 0, "input must be non-empty");
-  const c10::DeviceGuard device_guard(input.device());
-  at::Tensor output = at::empty({}, input.options());
-  check_launch(operatorlib::reduce_sum_f32(
-                   input.data_ptr<float>(), output.data_ptr<float>(),
-                   static_cast<std::size_t>(input.numel()),
-                   current_stream(input)),
-               "reduce_sum");
-  return output;
+const void* caddr(const at::Tensor& t) { return t.data_ptr(); }
+
+// Runs `call(stream)` (one C ABI entry point) with the inputs' device
+// current, on that device's current stream.
+template <typename Call>
+void launch(const Operands& in, Call&& call) {
+  const c10::DeviceGuard guard(in.lead().device());
+  void* stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(
+                     in.lead().get_device()).stream();
+  const int status = call(stream);
+  TORCH_CHECK(status == 0, in.op(), " launch failed: ",
+              operatorlib_status_string(status));
 }
 
-// softmax and rmsnorm also take float16 tensors (output float16, fp32
-// arithmetic inside): the reference binding accepts float32 only
-// (operatorlib_binding.cpp:60, :96) and defers FP16 to a later dtype
-// extension (docs/pytorch_extension.md:143-146). Other dtypes still fail
-// with a message naming float32.
-at::Tensor softmax_hip(const at::Tensor& input) {
-  check_cuda_contiguous(input, "input");
-  const bool half = input.scalar_type() == at::kHalf;
-  TORCH_CHECK(input.scalar_type() == at::kFloat || half,
-              "softmax supports float32 or float16 input only");
-  TORCH_CHECK(input.dim() >= 1, "input must have at least one dimension");
-  const int cols = checked_positive_int(input.size(-1), "last dimension");
-  const int rows =
-      checked_positive_int(input.numel() / input.size(-1), "row count");
-  const c10::DeviceGuard device_guard(input.device());
-  at::Tensor output = at::empty_like(input);
-  if (half)
-    check_launch(operatorlib::softmax_f16(
-                     reinterpret_cast<const __half*>(input.data_ptr<at::Half>()),
-                     reinterpret_cast<__half*>(output.data_ptr<at::Half>()),
-                     rows, cols, current_stream(input)),
-                 "softmax");
-  else
-    check_launch(operatorlib::softmax_f32(input.data_ptr<float>(),
-                                          output.data_ptr<float>(), rows, cols,
-                                          current_stream(input)),
-                 "softmax");
-  return output;
+at::Tensor reduce_sum_op(const at::Tensor& input) {
+  const Operands in("reduce_sum", kFloat32Only, {{&input, "input"}});
+  TORCH_CHECK(input.numel() > 0, "reduce_sum: input must not be empty");
+  at::Tensor out = at::empty({}, input.options());
+  launch(in, [&](void* s) {
+    return operatorlib_reduce_sum_f32(static_cast<const float*>(caddr(input)),
+                                      static_cast<float*>(out.data_ptr()),
+                                      static_cast<size_t>(input.numel()), s);
+  });
+  return out;
 }
 
-at::Tensor transpose_hip(const at::Tensor& input) {
-  check_cuda_contiguous(input, "input");
-  TORCH_CHECK(input.scalar_type() == at::kFloat,
-              "transpose supports float32 input only");
-  TORCH_CHECK(input.dim() == 2, "input must be a 2D matrix");
-  const int rows = checked_positive_int(input.size(0), "rows");
-  const int cols = checked_positive_int(input.size(1), "cols");
-  const c10::DeviceGuard device_guard(input.device());
-  at::Tensor output = at::empty({cols, rows}, input.options());
-  check_launch(operatorlib::transpose_f32(input.data_ptr<float>(),
-                                          output.data_ptr<float>(), rows, cols,
-                                          current_stream(input)),
-               "transpose");
-  return output;
+// softmax and rmsnorm also accept float16 (fp32 arithmetic, float16
+// output): the reference binding takes float32 only
+// (operatorlib_binding.cpp:60, :96) and defers FP16
+// (docs/pytorch_extension.md:143-146).
+at::Tensor softmax_op(const at::Tensor& input) {
+  const Operands in("softmax", kFloat32OrFloat16, {{&input, "input"}});
+  const auto [rows, cols] = rows_by_last(in, input, "last dimension");
+  at::Tensor out = at::empty_like(input);
+  launch(in, [&](void* s) {
+    return in.half()
+               ? operatorlib_softmax_f16(
+                     static_cast<const operatorlib_half_t*>(caddr(input)),
+                     static_cast<operatorlib_half_t*>(out.data_ptr()), rows, cols, s)
+               : operatorlib_softmax_f32(static_cast<const float*>(caddr(input)),
+                                         static_cast<float*>(out.data_ptr()), rows,
+                                         cols, s);
+  });
+  return out;
 }
 
-at::Tensor rmsnorm_hip(const at::Tensor& input, const at::Tensor& weight,
-                       double epsilon) {
-  check_cuda_contiguous(input, "input");
-  check_cuda_contiguous(weight, "weight");
-  check_same_device_dtype(input, weight, "input", "weight");
-  const bool half = input.scalar_type() == at::kHalf;
-  TORCH_CHECK(input.scalar_type() == at::kFloat || half,
-              "rmsnorm supports float32 or float16 input only");
-  TORCH_CHECK(input.dim() >= 1, "input must have at least one dimension");
-  TORCH_CHECK(weight.dim() == 1, "weight must be 1D");
+at::Tensor transpose_op(const at::Tensor& input) {
+  const Operands in("transpose", kFloat32Only, {{&input, "input"}});
+  require_rank(in, input, "input", 2, "a 2D matrix");
+  const int rows = extent(in.op(), "rows", input.size(0));
+  const int cols = extent(in.op(), "cols", input.size(1));
+  at::Tensor out = at::empty({cols, rows}, input.options());
+  launch(in, [&](void* s) {
+    return operatorlib_transpose_f32(static_cast<const float*>(caddr(input)),
+                                     static_cast<float*>(out.data_ptr()), rows, cols, s);
+  });
+  return out;
+}
+
+at::Tensor rmsnorm_op(const at::Tensor& input, const at::Tensor& weight,
+                      double epsilon) {
+  const Operands in("rmsnorm", kFloat32OrFloat16,
+                    {{&input, "input"}, {&weight, "weight"}});
+  const auto [tokens, hidden] = rows_by_last(in, input, "hidden size");
+  require_rank(in, weight, "weight", 1, "a 1D vector");
+  TORCH_CHECK(weight.numel() == hidden, "rmsnorm: weight length ", weight.numel(),
+              " does not match the hidden size ", hidden);
   TORCH_CHECK(std::isfinite(epsilon) && epsilon > 0.0,
-              "epsilon must be finite and positive");
-  const int hidden = checked_positive_int(input.size(-1), "hidden size");
-  TORCH_CHECK(weight.numel() == hidden,
-              "weight length must equal the input hidden size");
-  const int tokens =
-      checked_positive_int(input.numel() / input.size(-1), "token count");
-  const c10::DeviceGuard device_guard(input.device());
-  at::Tensor output = at::empty_like(input);
-  if (half)
-    check_launch(operatorlib::rmsnorm_f16(
-                     reinterpret_cast<const __half*>(input.data_ptr<at::Half>()),
-                     reinterpret_cast<const __half*>(weight.data_ptr<at::Half>()),
-                     reinterpret_cast<__half*>(output.data_ptr<at::Half>()),
-                     tokens, hidden, static_cast<float>(epsilon),
-                     current_stream(input)),
-                 "rmsnorm");
-  else
-    check_launch(operatorlib::rmsnorm_f32(
-                     input.data_ptr<float>(), weight.data_ptr<float>(),
-                     output.data_ptr<float>(), tokens, hidden,
-                     static_cast<float>(epsilon), current_stream(input)),
-                 "rmsnorm");
-  return output;
+              "rmsnorm: epsilon must be finite and > 0, got ", epsilon);
+  const float eps = static_cast<float>(epsilon);
+  at::Tensor out = at::empty_like(input);
+  launch(in, [&](void* s) {
+    return in.half()
+               ? operatorlib_rmsnorm_f16(
+                     static_cast<const operatorlib_half_t*>(caddr(input)),
+                     static_cast<const operatorlib_half_t*>(caddr(weight)),
+                     static_cast<operatorlib_half_t*>(out.data_ptr()), tokens, hidden,
+                     eps, s)
+               : operatorlib_rmsnorm_f32(static_cast<const float*>(caddr(input)),
+                                         static_cast<const float*>(caddr(weight)),
+                                         static_cast<float*>(out.data_ptr()), tokens,
+                                         hidden, eps, s);
+  });
+  return out;
 }
 
-at::Tensor gemm_hip(const at::Tensor& a, const at::Tensor& b) {
-  check_cuda_contiguous(a, "a");
-  check_cuda_contiguous(b, "b");
-  check_same_device_dtype(a, b, "a", "b");
-  TORCH_CHECK(a.dim() == 2 && b.dim() == 2, "a and b must be 2D matrices");
-  TORCH_CHECK(a.size(1) == b.size(0), "a.size(1) must equal b.size(0)");
-  TORCH_CHECK(a.scalar_type() == at::kFloat || a.scalar_type() == at::kHalf,
-              "gemm supports float32 or float16 inputs only");
-  const int m = checked_positive_int(a.size(0), "M");
-  const int k = checked_positive_int(a.size(1), "K");
-  const int n = checked_positive_int(b.size(1), "N");
-  const c10::DeviceGuard device_guard(a.device());
-  at::Tensor output =
-      at::empty({m, n}, a.options().dtype(at::ScalarType::Float));
-  hipError_t error;
-  if (a.scalar_type() == at::kFloat) {
-    error = operatorlib::gemm_f32(a.data_ptr<float>(), b.data_ptr<float>(),
-                                  output.data_ptr<float>(), m, n, k,
-                                  current_stream(a));
-  } else {
-    error = operatorlib::gemm_f16(
-        reinterpret_cast<const __half*>(a.data_ptr<at::Half>()),
-        reinterpret_cast<const __half*>(b.data_ptr<at::Half>()),
-        output.data_ptr<float>(), m, n, k, current_stream(a));
-  }
-  check_launch(error, "gemm");
-  return output;
+at::Tensor gemm_op(const at::Tensor& a, const at::Tensor& b) {
+  const Operands in("gemm", kFloat32OrFloat16, {{&a, "a"}, {&b, "b"}});
+  require_rank(in, a, "a", 2, "a 2D matrix");
+  require_rank(in, b, "b", 2, "a 2D matrix");
+  TORCH_CHECK(a.size(1) == b.size(0), "gemm: a.size(1) = ", a.size(1),
+              " must equal b.size(0) = ", b.size(0));
+  const int m = extent(in.op(), "M", a.size(0));
+  const int k = extent(in.op(), "K", a.size(1));
+  const int n = extent(in.op(), "N", b.size(1));
+  at::Tensor out = at::empty({m, n}, a.options().dtype(at::kFloat));
+  launch(in, [&](void* s) {
+    float* c = static_cast<float*>(out.data_ptr());
+    return in.half()
+               ? operatorlib_gemm_f16(static_cast<const operatorlib_half_t*>(caddr(a)),
+                                      static_cast<const operatorlib_half_t*>(caddr(b)),
+                                      c, m, n, k, s)
+               : operatorlib_gemm_f32(static_cast<const float*>(caddr(a)),
+                                      static_cast<const float*>(caddr(b)), c, m, n, k, s);
+  });
+  return out;
 }
 
-at::Tensor attention_hip(const at::Tensor& q, const at::Tensor& k,
-                         const at::Tensor& v, bool causal) {
-  check_cuda_contiguous(q, "q");
-  check_cuda_contiguous(k, "k");
-  check_cuda_contiguous(v, "v");
-  check_same_device_dtype(q, k, "q", "k");
-  check_same_device_dtype(q, v, "q", "v");
-  TORCH_CHECK(q.dim() == 4, "q, k and v must use [B,H,S,D] layout");
-  TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(),
-              "q, k and v must have identical shapes");
-  TORCH_CHECK(q.scalar_type() == at::kFloat || q.scalar_type() == at::kHalf,
-              "attention supports float32 or float16 inputs only");
-  const int batch = checked_positive_int(q.size(0), "batch");
-  const int heads = checked_positive_int(q.size(1), "heads");
-  const int sequence = checked_positive_int(q.size(2), "sequence");
-  const int head_dim = checked_positive_int(q.size(3), "head dimension");
-  TORCH_CHECK(head_dim <= 128, "head dimension must be at most 128");
-  TORCH_CHECK(static_cast<int64_t>(batch) * heads <=
-                  std::numeric_limits<int>::max(),
-              "batch * heads exceeds the supported int32 range");
-  const c10::DeviceGuard device_guard(q.device());
-  at::Tensor output =
-      at::empty(q.sizes(), q.options().dtype(at::ScalarType::Float));
-  hipError_t error;
-  if (q.scalar_type() == at::kFloat) {
-    error = operatorlib::attention_f32(
-        q.data_ptr<float>(), k.data_ptr<float>(), v.data_ptr<float>(),
-        output.data_ptr<float>(), batch, heads, sequence, head_dim, causal,
-        current_stream(q));
-  } else {
-    error = operatorlib::attention_f16(
-        reinterpret_cast<const __half*>(q.data_ptr<at::Half>()),
-        reinterpret_cast<const __half*>(k.data_ptr<at::Half>()),
-        reinterpret_cast<const __half*>(v.data_ptr<at::Half>()),
-        output.data_ptr<float>(), batch, heads, sequence, head_dim, causal,
-        current_stream(q));
-  }
-  check_launch(error, "attention");
-  return output;
+at::Tensor attention_op(const at::Tensor& q, const at::Tensor& k,
+                        const at::Tensor& v, bool causal) {
+  const Operands in("attention", kFloat32OrFloat16, {{&q, "q"}, {&k, "k"}, {&v, "v"}});
+  require_rank(in, q, "q", 4, "[B,H,S,D]");
+  TORCH_CHECK(k.sizes() == q.sizes() && v.sizes() == q.sizes(),
+              "attention: q, k and v must have the same shape, got ", q.sizes(), ", ",
+              k.sizes(), ", ", v.sizes());
+  const int batch = extent(in.op(), "batch", q.size(0));
+  const int heads = extent(in.op(), "heads", q.size(1));
+  const int seq = extent(in.op(), "sequence", q.size(2));
+  const int dim = extent(in.op(), "head dimension", q.size(3));
+  TORCH_CHECK(dim <= 128, "attention: head dimension ", dim,
+              " is not supported (at most 128)");
+  TORCH_CHECK(static_cast<std::int64_t>(batch) * heads <= std::numeric_limits<int>::max(),
+              "attention: batch * heads = ", static_cast<std::int64_t>(batch) * heads,
+              " is not a positive int32");
+  at::Tensor out = at::empty(q.sizes(), q.options().dtype(at::kFloat));
+  launch(in, [&](void* s) {
+    float* o = static_cast<float*>(out.data_ptr());
+    const int c = causal ? 1 : 0;
+    return in.half()
+               ? operatorlib_attention_f16(
+                     static_cast<const operatorlib_half_t*>(caddr(q)),
+                     static_cast<const operatorlib_half_t*>(caddr(k)),
+                     static_cast<const operatorlib_half_t*>(caddr(v)), o, batch, heads,
+                     seq, dim, c, s)
+               : operatorlib_attention_f32(static_cast<const float*>(caddr(q)),
+                                           static_cast<const float*>(caddr(k)),
+                                           static_cast<const float*>(caddr(v)), o, batch,
+                                           heads, seq, dim, c, s);
+  });
+  return out;
 }
 
 }  // namespace
@@ -229,10 +252,10 @@ TORCH_LIBRARY(operatorlib, m) {
 }
 
 TORCH_LIBRARY_IMPL(operatorlib, CUDA, m) {
-  m.impl("reduce_sum", &reduce_sum_hip);
-  m.impl("softmax", &softmax_hip);
-  m.impl("transpose", &transpose_hip);
-  m.impl("rmsnorm", &rmsnorm_hip);
-  m.impl("gemm", &gemm_hip);
-  m.impl("attention", &attention_hip);
+  m.impl("reduce_sum", &reduce_sum_op);
+  m.impl("softmax", &softmax_op);
+  m.impl("transpose", &transpose_op);
+  m.impl("rmsnorm", &rmsnorm_op);
+  m.impl("gemm", &gemm_op);
+  m.impl("attention", &attention_op);
 }

@@ -1,21 +1,25 @@
 """operatorlib for MI355X — Python entry points.
 
 * ``load_operatorlib()`` registers ``torch.ops.operatorlib.{reduce_sum,
-  softmax, transpose, rmsnorm, gemm, attention}`` from the prebuilt in-tree
-  extension. It mirrors the reference's ``python/load_extension.py:17-36``
-  (which JIT-compiled CUDA sources); here the HIP build happens ahead of time
-  (``build()``) and loading never compiles anything.
+  softmax, transpose, rmsnorm, gemm, attention}`` from the in-tree
+  extension. Like the reference's ``python/load_extension.py:17-36``, which
+  compiles its CUDA sources on first use, it builds the HIP library and the
+  binding with hipcc for gfx950 when they are not built yet
+  (``OPERATORLIB_NO_BUILD=1`` turns that off); a build that exists is loaded
+  as it is.
 * ``clib()`` returns the ``ctypes`` handle of ``liboperatorlib.so`` with the
   C ABI of ``include/operatorlib/operatorlib_c.h`` typed, for callers that
-  want the library without the torch layer.
+  want the library without the torch layer. It builds on first use in the
+  same way.
 
-Both raise if the native library has not been built: there is no fallback
-implementation.
+Both raise if the native library is missing and cannot be built: there is
+no fallback implementation.
 """
 
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 from . import _build
@@ -64,18 +68,32 @@ def build(verbose: bool = False, torch_binding: bool = True) -> None:
     _build.build(verbose=verbose, torch_binding=torch_binding)
 
 
-def _require(path: Path) -> None:
-    if not path.exists():
+def _require(path: Path, torch_binding: bool) -> None:
+    """Build the native artefacts if `path` is missing; raise if that is not
+    possible."""
+    if path.exists():
+        return
+    if os.environ.get("OPERATORLIB_NO_BUILD", "0") == "1":
         raise RuntimeError(
-            f"operatorlib native library missing: {path}. Build it first "
-            "(python -c 'import __graft_entry__ as g; g.build()').")
+            f"operatorlib native library missing: {path} (OPERATORLIB_NO_BUILD=1). "
+            "Build it with python -c 'import __graft_entry__ as g; g.build()'.")
+    try:
+        if torch_binding:
+            _build.build(torch_binding=True)
+        else:
+            _build.build_library()
+    except Exception as exc:  # no silent fallback: report and stop
+        raise RuntimeError(f"operatorlib native library missing: {path}, and building "
+                           f"it failed: {exc}") from exc
+    if not path.exists():
+        raise RuntimeError(f"operatorlib build did not produce {path}")
 
 
 def clib() -> ctypes.CDLL:
     """Load ``liboperatorlib.so`` and type its C ABI."""
     global _clib
     if _clib is None:
-        _require(LIBRARY_PATH)
+        _require(LIBRARY_PATH, torch_binding=False)
         try:
             # Share the HIP runtime torch already loaded (same SONAME) when
             # torch is importable, so both use one runtime instance.
@@ -97,7 +115,7 @@ def load_operatorlib(verbose: bool = False) -> None:
     if _torch_loaded:
         return
     import torch
-    _require(TORCH_EXT_PATH)
+    _require(TORCH_EXT_PATH, torch_binding=True)
     clib()  # the extension links liboperatorlib.so; load it first, same runtime
     torch.ops.load_library(str(TORCH_EXT_PATH))
     if verbose:

@@ -37,8 +37,12 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # machines this library is tested on. hipcc's host pass warns that it does not
 # know the feature; that warning is filtered below.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Line tables (the reference builds with -lineinfo, CMakeLists.txt:30-32) let
+# rocprofv3 and other tools map samples to source lines; the gfx950
+# instruction stream is the same with and without them.
+LINE_TABLES = [] if os.environ.get("OPERATORLIB_LINE_TABLES", "1") == "0" else ["-gline-tables-only"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
-                "-I", str(INCLUDE), "-I", str(CSRC)] + DEVICE_FLAGS
+                "-I", str(INCLUDE), "-I", str(CSRC)] + DEVICE_FLAGS + LINE_TABLES
 
 LIB_SOURCES = [
     "reduce.hip", "softmax.hip", "rmsnorm.hip", "transpose.hip",
@@ -123,6 +127,23 @@ def build_runner(verbose: bool = False) -> Path:
           "-Wl,-rpath,$ORIGIN", "-o", str(tmp)], verbose)
     os.replace(tmp, RUNNER)
     return RUNNER
+
+
+CMAKE_BUILD_DIR = REPO_ROOT / "build" / "cmake"
+
+
+def build_cmake(verbose: bool = False, build_dir: Path = CMAKE_BUILD_DIR) -> Path:
+    """Configure and build the CMake project (CMakeLists.txt at the repository
+    root): liboperatorlib for C++ consumers, the runner, and the smoke
+    programs that ``ctest --test-dir <build_dir>`` runs."""
+    cmake = shutil.which("cmake")
+    if cmake is None:
+        raise RuntimeError("cmake not found")
+    generator = ["-G", "Ninja"] if shutil.which("ninja") else []
+    _run([cmake, "-S", str(REPO_ROOT), "-B", str(build_dir), *generator,
+          f"-DCMAKE_HIP_ARCHITECTURES={ARCH}", "-DCMAKE_BUILD_TYPE=Release"], verbose)
+    _run([cmake, "--build", str(build_dir), "-j", str(_jobs())], verbose)
+    return build_dir
 
 
 def build(verbose: bool = False, torch_binding: bool = True) -> None:
