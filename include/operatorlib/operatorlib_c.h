@@ -47,6 +47,25 @@ int operatorlib_reduce_sum_f32(const float* input, float* output, size_t n,
                                void* stream);
 
 /*
+ * operatorlib_reduce_sum_f32 without any allocation: the same kernels and
+ * the same result bits, with the per-workgroup partials in a static device
+ * array of 256 doubles (2 KiB per GPU, held until the process ends) instead
+ * of library scratch. No hipMalloc, no hipFree, no allocating library call,
+ * on any call, so callers that cannot allocate (code under HIP graph
+ * capture that forbids it, tight serving loops, harnesses that forbid
+ * allocation) can use it. Any n is accepted: the grid is capped at 256
+ * workgroups, one partial each.
+ * Every call on a GPU shares that GPU's array: calls whose executions
+ * overlap on one GPU (different streams, or different host threads) race
+ * and may return wrong sums; serialize them (one stream, one thread).
+ * Errors: as operatorlib_reduce_sum_f32.
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate.
+ */
+int operatorlib_reduce_sum_f32_noalloc(const float* input, float* output,
+                                       size_t n, void* stream);
+
+/*
  * Row-wise numerically stable softmax of a row-major [rows, cols] matrix.
  * Errors: NULL pointer, rows <= 0, cols <= 0.
  * Replaces operatorlib::softmax_f32, reference src/softmax.cu:182-202.

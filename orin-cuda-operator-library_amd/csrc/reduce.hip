@@ -16,6 +16,10 @@
 //     fp32 result (stream order makes pass 1's partials visible).
 // Inputs that fit one workgroup skip pass 2. No memset, no float atomics.
 //
+// operatorlib_reduce_sum_f32_noalloc runs the same two kernels with the
+// partials in a file-scope device array (`scratch`, 2 KiB per GPU) instead
+// of library scratch, so it never allocates.
+//
 // Why two launches: combining in the same launch needs each workgroup to
 // publish its partial at device scope and count arrivals. With a release
 // fence that costs an L2 writeback per workgroup (~300 us for 2048
@@ -32,6 +36,8 @@
 #include <algorithm>
 #include <cstddef>
 #include <cstdint>
+#include <map>
+#include <mutex>
 
 #include "common.hpp"
 #include "operatorlib/operatorlib_c.h"
@@ -120,35 +126,93 @@ __global__ __launch_bounds__(kCombineThreads) void reduce_combine_kernel(
   if (threadIdx.x == 0) output[0] = static_cast<float>(total);
 }
 
+// Grid of one call: the scalar head before the first 16-byte boundary, the
+// float4 body, and the number of pass-1 workgroups (at most kGridBlocks).
+struct Plan {
+  std::size_t head;
+  std::size_t nvec;
+  int blocks;
+};
+
+Plan plan_for(const float* input, std::size_t n) {
+  const std::uintptr_t address = reinterpret_cast<std::uintptr_t>(input);
+  Plan p;
+  p.head = std::min<std::size_t>(((16u - (address & 15u)) & 15u) / sizeof(float), n);
+  p.nvec = (n - p.head) / 4;
+  const std::size_t chunk = static_cast<std::size_t>(kThreads) * kUnroll;
+  const std::size_t wanted = std::max<std::size_t>(1, (p.nvec + chunk - 1) / chunk);
+  p.blocks = static_cast<int>(std::min<std::size_t>(wanted, kGridBlocks));
+  return p;
+}
+
+// Pass 1 and, for more than one workgroup, pass 2 over `partials` (at least
+// p.blocks doubles; unused for one workgroup).
+hipError_t enqueue(const float* input, float* output, std::size_t n, const Plan& p,
+                   double* partials, hipStream_t stream) {
+  reduce_partials_kernel<<<p.blocks, kThreads, 0, stream>>>(input, output, n, p.head,
+                                                            p.nvec, partials);
+  if (p.blocks > 1)
+    reduce_combine_kernel<<<1, kCombineThreads, 0, stream>>>(partials, p.blocks,
+                                                             output);
+  return hipGetLastError();
+}
+
+// Partials of operatorlib_reduce_sum_f32_noalloc: one array per GPU, held
+// from the library's load to process exit. A call's pass 1 writes every
+// slot pass 2 reads, so nothing in it has to start at zero.
+static __device__ __align__(256) double scratch[kGridBlocks];
+
+// Device address of `scratch` on the current device. The name `scratch` in
+// host code is a host-side stand-in, so kernels get this address instead;
+// it is looked up once per device, with that device current.
+hipError_t scratch_on_current_device(double** out) {
+  int device = 0;
+  hipError_t status = hipGetDevice(&device);
+  if (status != hipSuccess) return status;
+  static std::mutex mutex;
+  static std::map<int, double*> by_device;
+  std::lock_guard<std::mutex> lock(mutex);
+  const auto found = by_device.find(device);
+  if (found != by_device.end()) {
+    *out = found->second;
+    return hipSuccess;
+  }
+  double* ptr = nullptr;
+  status = hipGetSymbolAddress(reinterpret_cast<void**>(&ptr), HIP_SYMBOL(scratch));
+  if (status != hipSuccess) return status;
+  by_device.emplace(device, ptr);
+  *out = ptr;
+  return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" int operatorlib_reduce_sum_f32(const float* input, float* output,
                                           size_t n, void* stream_handle) {
   if (!opl::reduce_args_ok(input, output, n)) return hipErrorInvalidValue;
   hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-  const std::uintptr_t address = reinterpret_cast<std::uintptr_t>(input);
-  std::size_t head = ((16u - (address & 15u)) & 15u) / sizeof(float);
-  head = std::min(head, n);
-  const std::size_t nvec = (n - head) / 4;
-  const std::size_t chunk = static_cast<std::size_t>(kThreads) * kUnroll;
-  const std::size_t wanted = std::max<std::size_t>(
-      1, (nvec + chunk - 1) / chunk);
-  const int blocks = static_cast<int>(
-      std::min<std::size_t>(wanted, kGridBlocks));
-  if (blocks == 1) {
-    reduce_partials_kernel<<<1, kThreads, 0, stream>>>(input, output, n, head,
-                                                       nvec, nullptr);
-    return hipGetLastError();
-  }
+  const Plan p = plan_for(input, n);
+  if (p.blocks == 1) return enqueue(input, output, n, p, nullptr, stream);
   // Held until the combine kernel is enqueued (scratch.hpp).
   opl::ScratchLease lease(stream);
-  opl::Scratch scratch;
-  const hipError_t status = lease.get(sizeof(double) * kGridBlocks, &scratch);
+  opl::Scratch partials;
+  const hipError_t status = lease.get(sizeof(double) * kGridBlocks, &partials);
   if (status != hipSuccess) return status;
-  double* partials = static_cast<double*>(scratch.data);
-  reduce_partials_kernel<<<blocks, kThreads, 0, stream>>>(input, output, n,
-                                                          head, nvec, partials);
-  reduce_combine_kernel<<<1, kCombineThreads, 0, stream>>>(partials, blocks,
-                                                           output);
-  return hipGetLastError();
+  return enqueue(input, output, n, p, static_cast<double*>(partials.data), stream);
+}
+
+extern "C" int operatorlib_reduce_sum_f32_noalloc(const float* input, float* output,
+                                                  size_t n, void* stream_handle) {
+  if (!opl::reduce_args_ok(input, output, n)) return hipErrorInvalidValue;
+  hipStream_t stream = static_cast<hipStream_t>(stream_handle);
+  const Plan p = plan_for(input, n);
+  // The grid never exceeds kGridBlocks workgroups, so every n fits the
+  // kGridBlocks partials of `scratch`: there is no size to reject.
+  static_assert(sizeof(scratch) == sizeof(double) * kGridBlocks, "one slot per workgroup");
+  double* partials = nullptr;
+  if (p.blocks > 1) {
+    const hipError_t status = scratch_on_current_device(&partials);
+    if (status != hipSuccess) return status;
+  }
+  return enqueue(input, output, n, p, partials, stream);
 }

@@ -40,6 +40,8 @@ C_SYMBOLS = {
     "operatorlib_abi_version": (_c.c_int, []),
     "operatorlib_status_string": (_c.c_char_p, [_c.c_int]),
     "operatorlib_reduce_sum_f32": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "operatorlib_reduce_sum_f32_noalloc": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_size_t,
+                                                      _c.c_void_p]),
     "operatorlib_softmax_f32": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_void_p]),
     "operatorlib_softmax_f16": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_void_p]),
     "operatorlib_rmsnorm_f16": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int,

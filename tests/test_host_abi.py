@@ -62,7 +62,7 @@ def lib():
 
 def test_every_declared_symbol_is_exported(lib):
     names = declared_c_functions()
-    assert len(names) == 12, names
+    assert len(names) == 13, names
     assert set(names) == set(operatorlib.C_SYMBOLS)
     for name in names:
         assert hasattr(lib, name), name
@@ -107,10 +107,12 @@ def test_cpp_api_names_and_order():
 
 # -------------------------------------------------- validation before any HIP call
 
-def test_reduce_rejects(lib):
-    assert lib.operatorlib_reduce_sum_f32(NULL, FAKE, 10, NULL) == INVALID
-    assert lib.operatorlib_reduce_sum_f32(FAKE, NULL, 10, NULL) == INVALID
-    assert lib.operatorlib_reduce_sum_f32(FAKE, FAKE, 0, NULL) == INVALID
+@pytest.mark.parametrize("fn", ["operatorlib_reduce_sum_f32", "operatorlib_reduce_sum_f32_noalloc"])
+def test_reduce_rejects(lib, fn):
+    f = getattr(lib, fn)
+    assert f(NULL, FAKE, 10, NULL) == INVALID
+    assert f(FAKE, NULL, 10, NULL) == INVALID
+    assert f(FAKE, FAKE, 0, NULL) == INVALID
 
 
 @pytest.mark.parametrize("fn", ["operatorlib_softmax_f32", "operatorlib_softmax_f16",
