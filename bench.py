@@ -16,14 +16,24 @@ starts at the clocks the GPU holds under the load, not during its ramp),
 torch.cuda.synchronize(), a short untimed spin kernel (so the host queues
 every launch before the GPU reaches them), then K steps bracketed by one
 pair of HIP events recorded on the launch stream, then synchronize.
-Per-kernel durations (roofline, ops) come from separate regions of
+The roofline kernel's average launch comes from a separate region of
 back-to-back launches of that kernel, timed the same way.
 
 `roofline` covers the dominant kernel (RMSNorm, 2/3 of the step's bytes).
 `cpu_baseline` times the oracle's single-threaded C restatement of the
 reference CPU paths (softmax/softmax_v4.cu:253-268,
-rmsnorm/rmsnorm_v3.cu:154-172) on the same workload. `ops` holds every
-other BASELINE.json config, measured the same way.
+rmsnorm/rmsnorm_v3.cu:154-172) on the same workload, built on the GPU
+box's host with gcc -O3 -march=native.
+
+`ops` holds every other BASELINE.json config plus streaming ceilings
+(calibration/stream.hip) at the operators' sizes. Each entry's `ms` (and
+its throughput) is the mean launch over an event-free region of
+back-to-back launches; `group_ms` gives the median, min and p90 of the
+mean launch in groups of eight, with an event between groups only (an
+event after every launch would add ~2.7 us to each). The per-dispatch
+distribution, with no events at all, comes from the rocprofv3 kernel
+trace (profiles/). `cpu_ops` times the oracle on every config (one core),
+`cpu_torch_ops` PyTorch-CPU on every config (all of torch's threads).
 """
 
 from __future__ import annotations
@@ -43,7 +53,7 @@ sys.path.insert(0, str(REPO))
 sys.path.insert(0, str(REPO / "orin-cuda-operator-library_amd"))
 
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
-FP16_PEAK_TFLOPS = 2500.0       # dense FP16 MFMA (AMD lists 2516.6)
+FP16_PEAK_TFLOPS = 2516.6       # dense FP16 MFMA (AMD's MI355X figure)
 FP32_PEAK_TFLOPS = 157.3        # FP32 matrix
 # Cold-cache rotation: consecutive launches cycle through enough buffer sets
 # that the bytes READ per cycle are at least 4x the 256 MB MALL. Reads, not
@@ -54,6 +64,46 @@ FP32_PEAK_TFLOPS = 157.3        # FP32 matrix
 ROTATE_READ_BYTES = 1 << 30
 
 METRIC = "HBM GB/s for reduce/softmax/RMSNorm/transpose; TFLOP/s for GEMM/attention"
+
+
+def _kernel_label(name: str) -> str:
+    """`ns::kernel<args>` from a (possibly mangled) kernel-trace name."""
+    import shutil
+    import subprocess
+    if name.startswith("_Z") and shutil.which("c++filt"):
+        name = subprocess.run(["c++filt", name], capture_output=True, text=True).stdout.strip()
+    name = name.replace("(anonymous namespace)::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for i, ch in enumerate(name):  # drop the parameter list
+        depth += ch == "<"
+        depth -= ch == ">"
+        if ch == "(" and depth == 0 and i > 0:
+            return name[:i]
+    return name
+
+
+def summarize_trace(csv_path: str) -> None:
+    """Per-dispatch duration distribution (median, min, p90, mean, in us)
+    of every kernel and grid in a rocprofv3 kernel-trace CSV, as a markdown
+    table: the event-free per-launch figures the profiles quote."""
+    import csv
+    from collections import defaultdict
+    groups = defaultdict(list)
+    with open(csv_path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            grid = int(row.get("Grid_Size_X", row.get("Grid_Size", 0)) or 0)
+            wg = int(row.get("Workgroup_Size_X", row.get("Workgroup_Size", 0)) or 0)
+            dur = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
+            groups[(row["Kernel_Name"], grid, wg)].append(dur)
+    print("| kernel | grid (threads) | workgroup | calls | median us | min us | p90 us | mean us |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|")
+    for (name, grid, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        d.sort()
+        p90 = d[min(len(d) - 1, int(round(0.9 * (len(d) - 1))))]
+        print(f"| `{_kernel_label(name)}` | {grid} | {wg} | {len(d)} | {float(np.median(d)):.2f} | "
+              f"{d[0]:.2f} | {p90:.2f} | {sum(d) / len(d):.2f} |")
 
 
 def parse_args():
@@ -70,6 +120,9 @@ def parse_args():
                    help="only run a few launches of one kernel (for rocprofv3 --pmc runs); "
                         "'copy' is a plain 64 MiB device copy used to calibrate byte counters")
     p.add_argument("--launches", type=int, default=5)
+    p.add_argument("--summarize-trace", default=None, metavar="CSV",
+                   help="print the per-dispatch duration table of a rocprofv3 kernel-trace "
+                        "CSV and exit (no GPU needed)")
     return p.parse_args()
 
 
@@ -127,6 +180,23 @@ def profile_only(torch, lib, oracle, ptr, op: str, launches: int) -> None:
             assert rc == 0, rc
     torch.cuda.synchronize()
     print(f"profile {op}: {launches} launches done", flush=True)
+
+
+def calibration_lib():
+    """The streaming calibration kernels (calibration/stream.hip)."""
+    import ctypes
+
+    from operatorlib import _build
+    if not _build.CALIBRATION.exists():
+        _build.build_calibration()
+    lib = ctypes.CDLL(str(_build.CALIBRATION))
+    for name in ("opl_calib_copy_f32", "opl_calib_read_f32"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.opl_calib_read_blocks.restype = ctypes.c_size_t
+    lib.opl_calib_read_blocks.argtypes = [ctypes.c_size_t]
+    return lib
 
 
 def spin(torch, ms: float = 30.0):
@@ -206,11 +276,45 @@ def warm_up(torch, launch, min_launches):
     return i
 
 
-def time_single(torch, launch, steps, warmup):
-    """(mean ms per launch, mean ms per launch) after the warm-up."""
+GROUP = 8  # launches per group in group_means_ms
+
+
+def group_means_ms(torch, launch, launches):
+    """Mean duration (ms) per launch of consecutive groups of GROUP
+    back-to-back launches, with one HIP event between groups only. An event
+    after every launch drains the queue each time and adds about 2.7 us to
+    every microsecond-scale launch (measured: softmax 4096x1024 8.7 us per
+    launch with an event after each, 6.0 us without); between groups of
+    eight that cost is spread over eight launches."""
+    groups = max(1, launches // GROUP)
+    torch.cuda.synchronize()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
+    spin(torch)
+    events[0].record()
+    i = 0
+    for g in range(groups):
+        for _ in range(GROUP):
+            launch(i)
+            i += 1
+        events[g + 1].record()
+    torch.cuda.synchronize()
+    return [events[g].elapsed_time(events[g + 1]) / GROUP for g in range(groups)]
+
+
+def time_launches(torch, launch, steps, warmup):
+    """Timing of one operator after the warm-up:
+    * ms_mean: the mean over one region of `steps` back-to-back launches
+      with no events in between (time_region); throughput uses it, as the
+      roofline figure does;
+    * ms_median, ms_min, ms_p90: the distribution of group_means_ms over
+      max(steps, 8 * GROUP) further launches. The per-dispatch distribution
+      (no events at all) is in the kernel-trace profiles."""
     warm_up(torch, launch, warmup)
-    ms = time_region(torch, launch, steps)
-    return ms, ms
+    mean = time_region(torch, launch, steps)
+    d = sorted(group_means_ms(torch, launch, max(steps, 8 * GROUP)))
+    p90 = d[min(len(d) - 1, int(round(0.9 * (len(d) - 1))))]
+    return {"ms_median": float(np.median(d)), "ms_min": d[0], "ms_p90": p90, "ms_mean": mean,
+            "launches": steps, "groups": len(d)}
 
 
 def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
@@ -220,18 +324,26 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
     stream = torch.cuda.current_stream().cuda_stream
     dev = "cuda"
 
-    def bw_entry(name, shape, nbytes, ms_med, ms_mean, ref_gbps=None):
-        gbps = nbytes / (ms_med * 1e-3) / 1e9
-        e = {"op": name, "shape": shape, "ms": round(ms_med, 5), "ms_mean": round(ms_mean, 5),
+    def timing_fields(t, digits):
+        return {"ms": round(t["ms_mean"], digits),
+                "group_ms": {"median": round(t["ms_median"], digits),
+                             "min": round(t["ms_min"], digits),
+                             "p90": round(t["ms_p90"], digits),
+                             "groups": t["groups"], "launches_per_group": GROUP},
+                "launches": t["launches"]}
+
+    def bw_entry(name, shape, nbytes, t, ref_gbps=None):
+        gbps = nbytes / (t["ms_mean"] * 1e-3) / 1e9
+        e = {"op": name, "shape": shape, **timing_fields(t, 5),
              "GBps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
              "bytes": nbytes}
         if ref_gbps:
             e["reference_orin_GBps"] = ref_gbps
         return e
 
-    def fl_entry(name, shape, flops, ms_med, ms_mean, peak, extra=None):
-        tf = flops / (ms_med * 1e-3) / 1e12
-        e = {"op": name, "shape": shape, "ms": round(ms_med, 4), "ms_mean": round(ms_mean, 4),
+    def fl_entry(name, shape, flops, t, peak, extra=None):
+        tf = flops / (t["ms_mean"] * 1e-3) / 1e12
+        e = {"op": name, "shape": shape, **timing_fields(t, 4),
              "TFLOPs": round(tf, 2), "roofline_frac": round(tf / peak, 4), "flops": flops}
         if extra:
             e.update(extra)
@@ -240,16 +352,32 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
     want = (lambda n: True) if names == "all" else (lambda n: n in names.split(","))
 
     if want("copy"):
-        # Not an operatorlib op: a plain 64 MiB device-to-device copy, the
-        # practical streaming ceiling the bandwidth kernels are read against.
+        # Not operatorlib ops: plain streams, the practical ceilings the
+        # bandwidth kernels are read against, timed the same way at the
+        # operators' sizes (calibration/stream.hip: non-temporal float4
+        # copy, and a read-only pass; torch's own device copy for reference).
+        calib = calibration_lib()
+        for mib in (16, 32, 64, 128):
+            n = mib * 2 ** 18  # fp32 elements in `mib` MiB
+            sets = sets_for(4 * n)
+            xs = [(torch.rand(n, device=dev), torch.empty(n, device=dev)) for _ in range(sets)]
+            f = lambda i: calib.opl_calib_copy_f32(ptr(xs[i % sets][0]), ptr(xs[i % sets][1]),
+                                                   n, stream)
+            out.append(bw_entry(f"stream_copy (calibration, {mib} MiB each way)", [n], 8 * n,
+                                time_launches(torch, f, steps, warmup)))
+            del xs
         n = 16 * 2 ** 20
         sets = sets_for(4 * n)
-        xs = [(torch.rand(n, device=dev), torch.empty(n, device=dev)) for _ in range(sets)]
+        xs = [torch.rand(n, device=dev) for _ in range(sets)]
+        part = torch.empty(calib.opl_calib_read_blocks(n), device=dev)
+        f = lambda i: calib.opl_calib_read_f32(ptr(xs[i % sets]), ptr(part), n, stream)
+        out.append(bw_entry("stream_read (calibration, 64 MiB read-only)", [n], 4 * n,
+                            time_launches(torch, f, steps, warmup)))
+        xs = [(x, torch.empty(n, device=dev)) for x in xs]
         f = lambda i: xs[i % sets][1].copy_(xs[i % sets][0])
-        e = bw_entry("device_copy (torch, ceiling reference)", [n], 8 * n,
-                     *time_single(torch, f, steps, warmup))
-        out.append(e)
-        del xs
+        out.append(bw_entry("device_copy (torch, 64 MiB each way)", [n], 8 * n,
+                            time_launches(torch, f, steps, warmup)))
+        del xs, part
 
     if want("reduce"):
         n = 16_777_216
@@ -258,7 +386,7 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         xs = [x.cuda() for _ in range(sets)]
         y = torch.empty(1, device=dev)
         f = lambda i: lib.operatorlib_reduce_sum_f32(ptr(xs[i % sets]), ptr(y), n, stream)
-        out.append(bw_entry("reduce_sum_f32", [n], 4 * n, *time_single(torch, f, steps, warmup),
+        out.append(bw_entry("reduce_sum_f32", [n], 4 * n, time_launches(torch, f, steps, warmup),
                             ref_gbps=93.67))
         del xs
 
@@ -271,7 +399,7 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         xs = [(x.cuda(), torch.empty(shape, device=dev)) for _ in range(sets)]
         f = lambda i: lib.operatorlib_softmax_f32(ptr(xs[i % sets][0]), ptr(xs[i % sets][1]),
                                                   shape[0], shape[1], stream)
-        out.append(bw_entry(name, list(shape), nb, *time_single(torch, f, steps, warmup), ref))
+        out.append(bw_entry(name, list(shape), nb, time_launches(torch, f, steps, warmup), ref))
         del xs
 
     for name, shape, ref in (("rmsnorm_f32", (2048, 4096), 94.83), ("rmsnorm_f32", (2047, 4095), None)):
@@ -284,7 +412,7 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         xs = [(x.cuda(), torch.empty(shape, device=dev)) for _ in range(sets)]
         f = lambda i: lib.operatorlib_rmsnorm_f32(ptr(xs[i % sets][0]), ptr(w), ptr(xs[i % sets][1]),
                                                   shape[0], shape[1], 1e-6, stream)
-        out.append(bw_entry(name, list(shape), nb, *time_single(torch, f, steps, warmup), ref))
+        out.append(bw_entry(name, list(shape), nb, time_launches(torch, f, steps, warmup), ref))
         del xs
 
     # FP16 rows (fp32 arithmetic inside): the reference's deferred dtype
@@ -298,7 +426,7 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         xs = [(x.cuda(), torch.empty(shape, device=dev, dtype=torch.float16)) for _ in range(sets)]
         f = lambda i: lib.operatorlib_softmax_f16(ptr(xs[i % sets][0]), ptr(xs[i % sets][1]),
                                                   shape[0], shape[1], stream)
-        out.append(bw_entry(name, list(shape), nb, *time_single(torch, f, steps, warmup)))
+        out.append(bw_entry(name, list(shape), nb, time_launches(torch, f, steps, warmup)))
         del xs
 
     for name, shape in (("rmsnorm_f16", (2048, 4096)), ("rmsnorm_f16", (2047, 4095))):
@@ -311,7 +439,7 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         xs = [(x.cuda(), torch.empty(shape, device=dev, dtype=torch.float16)) for _ in range(sets)]
         f = lambda i: lib.operatorlib_rmsnorm_f16(ptr(xs[i % sets][0]), ptr(w), ptr(xs[i % sets][1]),
                                                   shape[0], shape[1], 1e-6, stream)
-        out.append(bw_entry(name, list(shape), nb, *time_single(torch, f, steps, warmup)))
+        out.append(bw_entry(name, list(shape), nb, time_launches(torch, f, steps, warmup)))
         del xs
 
     for name, shape, ref in (("transpose_f32", (4096, 4096), 94.34), ("transpose_f32", (4095, 4097), None)):
@@ -323,7 +451,7 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         xs = [(x.cuda(), torch.empty(shape[::-1], device=dev)) for _ in range(sets)]
         f = lambda i: lib.operatorlib_transpose_f32(ptr(xs[i % sets][0]), ptr(xs[i % sets][1]),
                                                     shape[0], shape[1], stream)
-        out.append(bw_entry(name, list(shape), nb, *time_single(torch, f, steps, warmup), ref))
+        out.append(bw_entry(name, list(shape), nb, time_launches(torch, f, steps, warmup), ref))
         del xs
 
     gemm_cases = [("gemm_f32", 4096, 1.191), ("gemm_f32", 4095, None), ("gemm_f16", 4096, 5.197),
@@ -346,7 +474,7 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         reps = max(5, min(steps, 20))
         extra = {"reference_orin_TFLOPs": ref} if ref else None
         out.append(fl_entry(name, [size, size, size], 2 * size ** 3,
-                            *time_single(torch, f, reps, 3), peak, extra))
+                            time_launches(torch, f, reps, 3), peak, extra))
         del da, db, c
 
     # Decode-shaped GEMMs (the reference's M == 1 and M <= 16 configurations):
@@ -366,10 +494,10 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         c = torch.empty((m, n), device=dev)
         fn = lib.operatorlib_gemm_f16 if es == 2 else lib.operatorlib_gemm_f32
         f = lambda i: fn(ptr(a), ptr(bs[i % sets]), ptr(c), m, n, k, stream)
-        ms_med, ms_mean = time_single(torch, f, steps, warmup)
+        t = time_launches(torch, f, steps, warmup)
         nbytes = (m * k + k * n) * es + m * n * 4
-        e = bw_entry(f"{name} skinny", [m, n, k], nbytes, ms_med, ms_mean)
-        e["TFLOPs"] = round(2 * m * n * k / (ms_med * 1e-3) / 1e12, 3)
+        e = bw_entry(f"{name} skinny", [m, n, k], nbytes, t)
+        e["TFLOPs"] = round(2 * m * n * k / (t["ms_mean"] * 1e-3) / 1e12, 3)
         out.append(e)
         del bs, a, c
 
@@ -387,11 +515,10 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         dense = 4 * bsz * heads * seq * seq * d
         eff = 4 * bsz * heads * d * seq * (seq + 1) // 2 if causal else dense
         reps = max(5, min(steps, 20))
-        ms_med, ms_mean = time_single(torch, f, reps, 3)
-        extra = {"dense_convention_TFLOPs": round(dense / (ms_med * 1e-3) / 1e12, 2),
+        t = time_launches(torch, f, reps, 3)
+        extra = {"dense_convention_TFLOPs": round(dense / (t["ms_mean"] * 1e-3) / 1e12, 2),
                  "causal": causal, "flops_convention": "effective (unmasked)"}
-        out.append(fl_entry("attention_f16", list(shape), eff, ms_med, ms_mean,
-                            FP16_PEAK_TFLOPS, extra))
+        out.append(fl_entry("attention_f16", list(shape), eff, t, FP16_PEAK_TFLOPS, extra))
         del qkv, o
     # FP32 attention (API coverage; no BASELINE config): the S1024 shape of
     # the FP16 configs, and a shape with enough workgroups to fill the GPU.
@@ -408,15 +535,15 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
                                                     bsz, heads, seq, d, int(causal), stream)
         dense = 4 * bsz * heads * seq * seq * d
         eff = 4 * bsz * heads * d * seq * (seq + 1) // 2 if causal else dense
-        ms_med, ms_mean = time_single(torch, f, max(5, min(steps, 20)), 3)
-        out.append(fl_entry("attention_f32", list(shape), eff, ms_med, ms_mean,
-                            FP32_PEAK_TFLOPS, {"causal": causal}))
+        t = time_launches(torch, f, max(5, min(steps, 20)), 3)
+        out.append(fl_entry("attention_f32", list(shape), eff, t, FP32_PEAK_TFLOPS,
+                            {"causal": causal}))
         del qkv, o
     torch.cuda.empty_cache()
     return out
 
 
-def cpu_baseline(oracle, budget_s: float):
+def cpu_baseline(oracle, budget_s: float, build_cmd: str):
     """The oracle (single-threaded C restatement of the reference CPU paths)
     on the headline workload, repeated until the time budget is used."""
     import numpy as np
@@ -435,11 +562,21 @@ def cpu_baseline(oracle, budget_s: float):
     gbps = done * step_bytes / el / 1e9
     return {"value": round(gbps, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{done} full steps (softmax 4096x1024 + rmsnorm 2048x4096) in {el:.1f} s, "
-                      f"oracle/oracle.c single thread, gcc -O3; host {platform.processor() or platform.machine()}, "
-                      f"nproc {os.cpu_count()}"}
+                      f"oracle/oracle.c single thread, built on this host: {build_cmd}; "
+                      f"host {cpu_model()}, nproc {os.cpu_count()}"}
 
 
-def cpu_ops_baseline(oracle):
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_ops_baseline(oracle, build_cmd: str):
     """Single-threaded oracle timings of every BASELINE config (reported
     beside the GPU figures, not a target). Bandwidth ops run in full (best
     of two calls); GEMM times a few rows of A against the full B, attention
@@ -486,7 +623,76 @@ def cpu_ops_baseline(oracle):
         del q, k, v
     entries = []
     for n, sh, ms, smp, *causal in out:
-        e = {"op": n, "shape": sh, "cpu_ms": round(ms, 3), "sample": smp, "cores": 1}
+        e = {"op": n, "shape": sh, "cpu_ms": round(ms, 3), "sample": smp, "cores": 1,
+             "build": build_cmd}
+        if causal:
+            e["causal"] = causal[0]
+        entries.append(e)
+    return entries
+
+
+def torch_cpu_ops(torch):
+    """PyTorch-CPU on every BASELINE config with all of torch's host threads
+    (reported beside the GPU figures, not a target; best of two calls).
+    Attention follows the reference's attention_reference
+    (python/test_extension.py:17-27) in fp32; B4 H32 S8192 is timed on four
+    heads and scaled to 128 (labelled). fp16 GEMM configs time the fp32
+    product of the fp16-rounded inputs (the reference's torch.matmul(a.float(),
+    b.float()), test_extension.py:90)."""
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(40)
+
+    def timed(fn, reps=2):
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            best = min(best, time.perf_counter() - t0)
+        return best * 1e3
+
+    out = []
+    x = torch.rand(16_777_216, generator=g) * 2 - 1
+    out.append(("reduce_sum_f32", [16_777_216], timed(lambda: x.sum()), "full"))
+    for shape in ((4096, 1024), (4097, 1023)):
+        x = torch.randn(shape, generator=g) * 3
+        out.append(("softmax_f32", list(shape), timed(lambda: torch.softmax(x, -1)), "full"))
+    for shape in ((2048, 4096), (2047, 4095)):
+        x = torch.randn(shape, generator=g)
+        w = torch.rand(shape[1], generator=g) + 0.5
+        f = lambda: x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1e-6) * w
+        out.append(("rmsnorm_f32", list(shape), timed(f), "full"))
+    for shape in ((4096, 4096), (4095, 4097)):
+        x = torch.rand(shape, generator=g)
+        out.append(("transpose_f32", list(shape), timed(lambda: x.t().contiguous()), "full"))
+    for name, size in (("gemm_f32", 4096), ("gemm_f32", 4095), ("gemm_f16", 4096),
+                       ("gemm_f16", 8192), ("gemm_f16", 4095)):
+        a = torch.rand((size, size), generator=g) * 2 - 1
+        b = torch.rand((size, size), generator=g) * 2 - 1
+        if name == "gemm_f16":
+            a, b = a.half().float(), b.half().float()
+        out.append((name, [size, size, size], timed(lambda: torch.matmul(a, b)), "full"))
+        del a, b
+
+    def attention_reference(q, k, v, causal):
+        scores = torch.matmul(q, k.transpose(-2, -1)) / (q.shape[-1] ** 0.5)
+        if causal:
+            s_len = q.shape[-2]
+            mask = torch.ones(s_len, s_len, dtype=torch.bool).triu(1)
+            scores = scores.masked_fill(mask, float("-inf"))
+        return torch.matmul(torch.softmax(scores, -1), v)
+
+    for bsz, heads, seq, causal, timed_heads in ((1, 12, 1024, False, 12), (1, 12, 1024, True, 12),
+                                                 (4, 32, 8192, True, 4)):
+        q, k, v = (torch.randn((1, timed_heads, seq, 128), generator=g) for _ in range(3))
+        ms = timed(lambda: attention_reference(q, k, v, causal)) * bsz * heads / timed_heads
+        sample = "full" if timed_heads == bsz * heads else \
+            f"{timed_heads} heads, scaled to {bsz * heads}"
+        out.append(("attention_f16", [bsz, heads, seq, 128], ms, sample, causal))
+        del q, k, v
+    entries = []
+    for n, sh, ms, smp, *causal in out:
+        e = {"op": n, "shape": sh, "torch_cpu_ms": round(ms, 3), "sample": smp,
+             "threads": threads}
         if causal:
             e["causal"] = causal[0]
         entries.append(e)
@@ -514,6 +720,9 @@ def torch_cpu_baseline(torch, budget_s: float):
 
 def main():
     args = parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
               "(each operator is a single-GPU kernel; sharding is not built).",
@@ -581,17 +790,29 @@ def main():
     cpu = None
     extra_cpu = None
     cpu_ops = None
+    torch_ops = None
     if not args.no_cpu:
-        cpu = cpu_baseline(oracle, args.cpu_seconds)
+        import tempfile
+        # The CPU baseline's build: gcc -O3 -march=native on this host.
+        build_cmd = oracle.use_native_build(tempfile.mkdtemp(prefix="oracle_native_"))
+        cpu = cpu_baseline(oracle, args.cpu_seconds, build_cmd)
         extra_cpu = torch_cpu_baseline(torch, min(5.0, args.cpu_seconds))
-        cpu_ops = cpu_ops_baseline(oracle)
-        # GPU / CPU-oracle ratio on the matching op entries
+        cpu_ops = cpu_ops_baseline(oracle, build_cmd)
+        torch_ops = torch_cpu_ops(torch)
+        # GPU / CPU ratios on the matching op entries
+        def match(o, c):
+            return (o["op"] == c["op"] and o["shape"] == c["shape"] and o.get("ms")
+                    and o.get("causal") == c.get("causal"))
         for c in cpu_ops:
             for o in ops:
-                if (o["op"] == c["op"] and o["shape"] == c["shape"] and o.get("ms")
-                        and o.get("causal") == c.get("causal")):
+                if match(o, c):
                     o["cpu_oracle_ms"] = c["cpu_ms"]
                     o["speedup_vs_cpu_oracle"] = round(c["cpu_ms"] / o["ms"], 1)
+        for c in torch_ops:
+            for o in ops:
+                if match(o, c):
+                    o["torch_cpu_ms"] = c["torch_cpu_ms"]
+                    o["speedup_vs_torch_cpu"] = round(c["torch_cpu_ms"] / o["ms"], 1)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -607,6 +828,7 @@ def main():
         "cpu_baseline": cpu,
         "cpu_torch": extra_cpu,
         "cpu_ops": cpu_ops,
+        "cpu_torch_ops": torch_ops,
         "ops": ops,
         "device": torch.cuda.get_device_name(0),
     }

@@ -39,6 +39,22 @@ def build() -> Path:
     return _LIB_PATH
 
 
+def use_native_build(directory) -> str:
+    """Compile oracle.c with ``-O3 -march=native`` into ``directory`` and
+    route every later oracle call through that build; returns the compile
+    command. The CPU baseline is quoted for this build.
+    ``-ffp-contract=off`` keeps the arithmetic exactly as written, so the
+    results are those of the portable build; only the speed differs."""
+    global _lib
+    out = Path(directory) / "liboracle_native.so"
+    cmd = ["gcc", "-O3", "-march=native", "-std=c11", "-fPIC", "-ffp-contract=off",
+           "-shared", "-o", str(out), str(_DIR / "oracle.c"), "-lm"]
+    subprocess.run(cmd, check=True)
+    with _lock:
+        _lib = _open(out)
+    return " ".join(cmd[:6]) + " oracle.c"
+
+
 def _load():
     global _lib
     with _lock:
@@ -47,26 +63,31 @@ def _load():
                          _LIB_PATH.stat().st_mtime < (_DIR / "oracle.c").stat().st_mtime)
             if src_newer:
                 build()
-            lib = ctypes.CDLL(str(_LIB_PATH))
-            sig = {
-                "oracle_fill_uniform": [_c.c_uint64, _c.c_float, _c.c_float, _P, _c.c_size_t],
-                "oracle_fill_normal": [_c.c_uint64, _c.c_float, _c.c_float, _P, _c.c_size_t],
-                "oracle_f32_to_f16_array": [_P, _P, _c.c_size_t],
-                "oracle_f16_to_f32_array": [_P, _P, _c.c_size_t],
-                "oracle_softmax": [_P, _P, _c.c_int, _c.c_int],
-                "oracle_transpose": [_P, _P, _c.c_int, _c.c_int],
-                "oracle_rmsnorm": [_P, _P, _P, _c.c_int, _c.c_int, _c.c_float],
-                "oracle_gemm": [_P, _P, _P, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int],
-                "oracle_attention": [_P, _P, _P, _P, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
-                                     _P, _P, _c.c_int],
-            }
-            for name, argtypes in sig.items():
-                getattr(lib, name).argtypes = argtypes
-                getattr(lib, name).restype = None
-            lib.oracle_reduce_sum.argtypes = [_P, _c.c_size_t]
-            lib.oracle_reduce_sum.restype = _c.c_double
-            _lib = lib
+            _lib = _open(_LIB_PATH)
     return _lib
+
+
+def _open(path):
+    """Load one build of oracle.c and type its functions."""
+    lib = ctypes.CDLL(str(path))
+    sig = {
+        "oracle_fill_uniform": [_c.c_uint64, _c.c_float, _c.c_float, _P, _c.c_size_t],
+        "oracle_fill_normal": [_c.c_uint64, _c.c_float, _c.c_float, _P, _c.c_size_t],
+        "oracle_f32_to_f16_array": [_P, _P, _c.c_size_t],
+        "oracle_f16_to_f32_array": [_P, _P, _c.c_size_t],
+        "oracle_softmax": [_P, _P, _c.c_int, _c.c_int],
+        "oracle_transpose": [_P, _P, _c.c_int, _c.c_int],
+        "oracle_rmsnorm": [_P, _P, _P, _c.c_int, _c.c_int, _c.c_float],
+        "oracle_gemm": [_P, _P, _P, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int],
+        "oracle_attention": [_P, _P, _P, _P, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                             _P, _P, _c.c_int],
+    }
+    for name, argtypes in sig.items():
+        getattr(lib, name).argtypes = argtypes
+        getattr(lib, name).restype = None
+    lib.oracle_reduce_sum.argtypes = [_P, _c.c_size_t]
+    lib.oracle_reduce_sum.restype = _c.c_double
+    return lib
 
 
 def _ptr(a: np.ndarray):

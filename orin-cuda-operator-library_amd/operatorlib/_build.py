@@ -116,6 +116,19 @@ def build_torch_binding(verbose: bool = False) -> Path:
     return TORCH_EXT
 
 
+CALIBRATION = LIB_DIR / "libopl_calibration.so"
+
+
+def build_calibration(verbose: bool = False) -> Path:
+    """HBM streaming kernels bench.py times beside the operators
+    (calibration/stream.hip); not part of the operatorlib ABI."""
+    src = PKG_ROOT / "calibration" / "stream.hip"
+    tmp = CALIBRATION.with_suffix(".so.tmp")
+    _run([HIPCC, *COMMON_FLAGS, "-shared", "-x", "hip", str(src), "-o", str(tmp)], verbose)
+    os.replace(tmp, CALIBRATION)
+    return CALIBRATION
+
+
 RUNNER = LIB_DIR / "operatorlib_run"
 
 
@@ -151,6 +164,7 @@ def build(verbose: bool = False, torch_binding: bool = True) -> None:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     build_library(verbose)
     build_runner(verbose)
+    build_calibration(verbose)
     if torch_binding:
         build_torch_binding(verbose)
 
