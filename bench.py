@@ -71,7 +71,10 @@ def _kernel_label(name: str) -> str:
     import shutil
     import subprocess
     if name.startswith("_Z") and shutil.which("c++filt"):
-        name = subprocess.run(["c++filt", name], capture_output=True, text=True).stdout.strip()
+        # binutils' c++filt does not know _Float16 (DF16_); spell it as half
+        # (Dh) for the demangler and rename it back.
+        name = subprocess.run(["c++filt", name.replace("DF16_", "Dh")], capture_output=True,
+                              text=True).stdout.strip().replace("half", "_Float16")
     name = name.replace("(anonymous namespace)::", "")
     if name.startswith("void "):
         name = name[5:]
@@ -80,8 +83,8 @@ def _kernel_label(name: str) -> str:
         depth += ch == "<"
         depth -= ch == ">"
         if ch == "(" and depth == 0 and i > 0:
-            return name[:i]
-    return name
+            return name[:i] if i <= 100 else name[:97] + "..."
+    return name if len(name) <= 100 else name[:97] + "..."
 
 
 def summarize_trace(csv_path: str) -> None:
@@ -116,9 +119,11 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="budget for the CPU baseline leg")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", default=None, choices=sorted(PROFILE_OPS),
-                   help="only run a few launches of one kernel (for rocprofv3 --pmc runs); "
-                        "'copy' is a plain 64 MiB device copy used to calibrate byte counters")
+    p.add_argument("--profile", default=None, metavar="OPS",
+                   help="only run a few launches of the listed kernels (comma list of "
+                        + ", ".join(sorted(PROFILE_OPS)) + ", or 'bandwidth' for every "
+                        "HBM-bound one) for rocprofv3 runs; 'copy' and 'stream_copy' are "
+                        "plain 64 MiB copies used to calibrate byte counters")
     p.add_argument("--launches", type=int, default=5)
     p.add_argument("--summarize-trace", default=None, metavar="CSV",
                    help="print the per-dispatch duration table of a rocprofv3 kernel-trace "
@@ -128,38 +133,69 @@ def parse_args():
 
 # --------------------------------------------------------------------- helpers
 
-PROFILE_OPS = {"copy", "reduce", "softmax", "rmsnorm", "transpose", "transpose_ragged",
+PROFILE_OPS = {"copy", "stream_copy", "reduce", "softmax", "softmax_ragged", "softmax_f16",
+               "softmax_f16_ragged", "rmsnorm", "rmsnorm_ragged", "rmsnorm_f16",
+               "rmsnorm_f16_ragged", "transpose", "transpose_ragged", "gemm_skinny",
                "gemm_f32", "gemm_f16", "attention_f16"}
+# Every HBM-bound kernel, for one counter pass that covers them all.
+BANDWIDTH_OPS = ["copy", "stream_copy", "reduce", "softmax", "softmax_ragged", "softmax_f16",
+                 "softmax_f16_ragged", "rmsnorm", "rmsnorm_ragged", "rmsnorm_f16",
+                 "rmsnorm_f16_ragged", "transpose", "transpose_ragged", "gemm_skinny"]
 
 
-def profile_only(torch, lib, oracle, ptr, op: str, launches: int) -> None:
-    """A few launches of one kernel at its benchmark size, nothing timed."""
+def profile_launchers(torch, lib, ptr, op: str):
+    """Launch closures of one profile op at its benchmark size(s)."""
     dev = "cuda"
     stream = torch.cuda.current_stream().cuda_stream
     gen = torch.Generator(device=dev).manual_seed(1)
     if op == "copy":
         x = torch.rand(16 * 2 ** 20, device=dev, generator=gen)  # 64 MiB
         y = torch.empty_like(x)
-        f = lambda: y.copy_(x)
-    elif op == "reduce":
+        return [lambda: y.copy_(x)]
+    if op == "stream_copy":
+        calib = calibration_lib()
+        x = torch.rand(16 * 2 ** 20, device=dev, generator=gen)  # 64 MiB
+        y = torch.empty_like(x)
+        return [lambda: calib.opl_calib_copy_f32(ptr(x), ptr(y), x.numel(), stream)]
+    if op == "reduce":
         x = torch.rand(16_777_216, device=dev, generator=gen)
         y = torch.empty(1, device=dev)
-        f = lambda: lib.operatorlib_reduce_sum_f32(ptr(x), ptr(y), x.numel(), stream)
-    elif op == "softmax":
-        x = torch.randn(4096, 1024, device=dev, generator=gen) * 3
+        return [lambda: lib.operatorlib_reduce_sum_f32(ptr(x), ptr(y), x.numel(), stream)]
+    if op.startswith("softmax"):
+        half = "f16" in op
+        rows, cols = (4097, 1023) if op.endswith("ragged") else (4096, 1024)
+        x = torch.randn(rows, cols, device=dev, generator=gen) * 3
+        x = x.half() if half else x
         y = torch.empty_like(x)
-        f = lambda: lib.operatorlib_softmax_f32(ptr(x), ptr(y), 4096, 1024, stream)
-    elif op == "rmsnorm":
-        x = torch.randn(2048, 4096, device=dev, generator=gen)
-        w = torch.rand(4096, device=dev, generator=gen) + 0.5
+        fn = lib.operatorlib_softmax_f16 if half else lib.operatorlib_softmax_f32
+        return [lambda: fn(ptr(x), ptr(y), rows, cols, stream)]
+    if op.startswith("rmsnorm"):
+        half = "f16" in op
+        rows, cols = (2047, 4095) if op.endswith("ragged") else (2048, 4096)
+        x = torch.randn(rows, cols, device=dev, generator=gen)
+        w = torch.rand(cols, device=dev, generator=gen) + 0.5
+        x, w = (x.half(), w.half()) if half else (x, w)
         y = torch.empty_like(x)
-        f = lambda: lib.operatorlib_rmsnorm_f32(ptr(x), ptr(w), ptr(y), 2048, 4096, 1e-6, stream)
-    elif op in ("transpose", "transpose_ragged"):
+        fn = lib.operatorlib_rmsnorm_f16 if half else lib.operatorlib_rmsnorm_f32
+        return [lambda: fn(ptr(x), ptr(w), ptr(y), rows, cols, 1e-6, stream)]
+    if op in ("transpose", "transpose_ragged"):
         rows, cols = (4096, 4096) if op == "transpose" else (4095, 4097)
         x = torch.rand(rows, cols, device=dev, generator=gen)
         y = torch.empty(cols, rows, device=dev)
-        f = lambda: lib.operatorlib_transpose_f32(ptr(x), ptr(y), rows, cols, stream)
-    elif op in ("gemm_f32", "gemm_f16"):
+        return [lambda: lib.operatorlib_transpose_f32(ptr(x), ptr(y), rows, cols, stream)]
+    if op == "gemm_skinny":  # decode GEMMs: M = 1 and 16, N = K = 4096, fp32 and fp16
+        out = []
+        for half in (False, True):
+            for m in (1, 16):
+                a = torch.rand(m, 4096, device=dev, generator=gen) * 2 - 1
+                b = torch.rand(4096, 4096, device=dev, generator=gen) * 2 - 1
+                a, b = (a.half(), b.half()) if half else (a, b)
+                c = torch.empty(m, 4096, device=dev)
+                fn = lib.operatorlib_gemm_f16 if half else lib.operatorlib_gemm_f32
+                out.append(lambda fn=fn, a=a, b=b, c=c, m=m:
+                           fn(ptr(a), ptr(b), ptr(c), m, 4096, 4096, stream))
+        return out
+    if op in ("gemm_f32", "gemm_f16"):
         n = 4096 if op == "gemm_f32" else 8192
         a = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
         b = torch.rand(n, n, device=dev, generator=gen) * 2 - 1
@@ -167,19 +203,30 @@ def profile_only(torch, lib, oracle, ptr, op: str, launches: int) -> None:
             a, b = a.half(), b.half()
         c = torch.empty(n, n, device=dev)
         fn = lib.operatorlib_gemm_f16 if op == "gemm_f16" else lib.operatorlib_gemm_f32
-        f = lambda: fn(ptr(a), ptr(b), ptr(c), n, n, n, stream)
-    else:  # attention_f16, B4 H32 S8192 D128 causal
-        shape = (4, 32, 8192, 128)
-        q, k, v = (torch.randn(shape, device=dev, generator=gen).half() for _ in range(3))
-        o = torch.empty(shape, device=dev)
-        f = lambda: lib.operatorlib_attention_f16(ptr(q), ptr(k), ptr(v), ptr(o), 4, 32, 8192,
-                                                  128, 1, stream)
-    for _ in range(launches):
-        rc = f()
-        if isinstance(rc, int):  # C ABI status (the copy returns a tensor)
-            assert rc == 0, rc
-    torch.cuda.synchronize()
-    print(f"profile {op}: {launches} launches done", flush=True)
+        return [lambda: fn(ptr(a), ptr(b), ptr(c), n, n, n, stream)]
+    # attention_f16, B4 H32 S8192 D128 causal
+    shape = (4, 32, 8192, 128)
+    q, k, v = (torch.randn(shape, device=dev, generator=gen).half() for _ in range(3))
+    o = torch.empty(shape, device=dev)
+    return [lambda: lib.operatorlib_attention_f16(ptr(q), ptr(k), ptr(v), ptr(o), 4, 32, 8192,
+                                                  128, 1, stream)]
+
+
+def profile_only(torch, lib, ptr, ops: str, launches: int) -> None:
+    """A few launches of each listed kernel at its benchmark size, nothing
+    timed (for rocprofv3 counter and trace runs). `ops` is a comma list of
+    PROFILE_OPS names, or "bandwidth" for every HBM-bound kernel."""
+    names = BANDWIDTH_OPS if ops == "bandwidth" else ops.split(",")
+    for op in names:
+        if op not in PROFILE_OPS:
+            raise SystemExit(f"bench.py: unknown --profile op {op!r}")
+        for f in profile_launchers(torch, lib, ptr, op):
+            for _ in range(launches):
+                rc = f()
+                if isinstance(rc, int):  # C ABI status (the torch copy returns a tensor)
+                    assert rc == 0, rc
+        torch.cuda.synchronize()
+        print(f"profile {op}: {launches} launches per launcher done", flush=True)
 
 
 def calibration_lib():
@@ -740,7 +787,7 @@ def main():
     import ctypes
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())
     if args.profile:
-        profile_only(torch, lib, oracle, ptr, args.profile, args.launches)
+        profile_only(torch, lib, ptr, args.profile, args.launches)
         return
 
     work = Rowwise(torch, lib, oracle, ptr)

@@ -14,12 +14,11 @@
 //   * transpose_vec4u_kernel (any other shape or alignment of at least 64
 //     such tiles, e.g. 4095x4097): the same 128x128 tiles with 16-byte
 //     accesses at 4-byte alignment, float4s crossing the matrix edge moved
-//     element by element. Measured on MI355X against the 4-byte kernel
-//     below (us): 4095x4097 42.3 -> 36.6, 4097x4095 35.9 -> 33.9, 4096x4096
-//     one element off alignment 41.1 -> 36.0, 8191x8193 157.3 -> 142.5.
-//     (Dealing each XCD a contiguous range of tiles, so that neighbours
-//     sharing boundary cache lines share an L2, was faster on three of these
-//     and slower on 4097x4095: 38.1 us.)
+//     element by element, and cache hints chosen by which side is
+//     misaligned (see vec4u_tile). Measured on MI355X against the 4-byte
+//     kernel below (us, both hints non-temporal): 4095x4097 42.3 -> 36.6,
+//     4097x4095 35.9 -> 33.9, 4096x4096 one element off alignment 41.1 ->
+//     36.0, 8191x8193 157.3 -> 142.5.
 //   * transpose_tile_kernel (smaller grids of any shape / alignment): a
 //     64x64 tile per 512-thread workgroup (8 wavefronts, 8 rows each)
 //     through a 64x65 LDS array; a wavefront reads one 256-byte input row
@@ -170,7 +169,21 @@ typedef float float4u __attribute__((ext_vector_type(4), aligned(4)));
 // handling is lighter): 129x257 3.2 vs 4.7 us, 1000x1000 equal at 5.1 us.
 constexpr long long kUnalignedMinTiles = 64;
 
-template <bool kFull>
+// Cache hints per side. Measured on MI355X (us; non-temporal loads /
+// stores vs the hints chosen here):
+//   input rows misaligned only: 4096x4095 29.51 -> 28.03 (cached loads),
+//     4096x4097 28.96 -> 27.53;
+//   output rows misaligned only: 4095x4096 31.36 -> 30.30 (cached stores),
+//     4097x4096 30.23 -> 29.87;
+//   both: 4095x4097 36.70 -> 35.21 (cached loads, non-temporal stores;
+//     cached stores as well: 37.10), 4097x4095 33.63 -> 31.93, 8191x8193
+//     142.61 -> 134.29.
+// Banding the tiles by XCD, so that tiles sharing a boundary line share an
+// L2, cut FETCH_SIZE at 4095x4097 from 1.27x to 1.00x of the input bytes
+// without changing the time (36.75 us): the misaligned 16-byte accesses
+// themselves, not re-fetched lines, set the cost. Coalesced 4-byte stores
+// for the misaligned output rows were slower (37.66 us).
+template <bool kFull, bool kLoadNT, bool kStoreNT>
 __device__ __forceinline__ void vec4u_tile(const float* __restrict__ input,
                                            float* __restrict__ output, int rows,
                                            int cols, int row0, int col0,
@@ -184,7 +197,8 @@ __device__ __forceinline__ void vec4u_tile(const float* __restrict__ input,
     const int c = col0 + 4 * (q % kRowChunks);
     const float* src = input + static_cast<std::size_t>(r) * cols + c;
     if (kFull || (r < rows && c + 3 < cols)) {
-      v[i] = __builtin_nontemporal_load(reinterpret_cast<const float4u*>(src));
+      v[i] = kLoadNT ? __builtin_nontemporal_load(reinterpret_cast<const float4u*>(src))
+                     : *reinterpret_cast<const float4u*>(src);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[i][j] = r < rows && c + j < cols ? src[j] : 0.0f;
@@ -211,7 +225,10 @@ __device__ __forceinline__ void vec4u_tile(const float* __restrict__ input,
     float* dst = output + static_cast<std::size_t>(c) * rows + r;
     if (kFull || (c < cols && r + 3 < rows)) {
       const float4v o = {s[0], s[kVecPitch], s[2 * kVecPitch], s[3 * kVecPitch]};
-      __builtin_nontemporal_store(o, reinterpret_cast<float4u*>(dst));
+      if (kStoreNT)
+        __builtin_nontemporal_store(o, reinterpret_cast<float4u*>(dst));
+      else
+        *reinterpret_cast<float4u*>(dst) = o;
     } else if (c < cols) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -220,6 +237,7 @@ __device__ __forceinline__ void vec4u_tile(const float* __restrict__ input,
   }
 }
 
+template <bool kLoadNT, bool kStoreNT>
 __global__ __launch_bounds__(kThreads) void transpose_vec4u_kernel(
     const float* __restrict__ input, float* __restrict__ output, int rows,
     int cols, int tiles_x, long long tiles) {
@@ -230,9 +248,9 @@ __global__ __launch_bounds__(kThreads) void transpose_vec4u_kernel(
     const int row0 = ty * kVecTile;
     const int col0 = tx * kVecTile;
     if (row0 + kVecTile <= rows && col0 + kVecTile <= cols)
-      vec4u_tile<true>(input, output, rows, cols, row0, col0, tile);
+      vec4u_tile<true, kLoadNT, kStoreNT>(input, output, rows, cols, row0, col0, tile);
     else
-      vec4u_tile<false>(input, output, rows, cols, row0, col0, tile);
+      vec4u_tile<false, kLoadNT, kStoreNT>(input, output, rows, cols, row0, col0, tile);
     if (t + gridDim.x < tiles) __syncthreads();  // tile is rewritten next
   }
 }
@@ -261,8 +279,17 @@ extern "C" int operatorlib_transpose_f32(const float* input, float* output,
       static_cast<long long>(vtiles_x) * ((rows + kVecTile - 1) / kVecTile);
   if (vtiles >= kUnalignedMinTiles) {
     const int blocks = static_cast<int>(vtiles < kMaxGrid ? vtiles : kMaxGrid);
-    transpose_vec4u_kernel<<<dim3(blocks), dim3(kThreads), 0, stream>>>(
-        input, output, rows, cols, vtiles_x, vtiles);
+    const dim3 grid(blocks), block(kThreads);
+    // Input rows are 16-byte aligned when cols % 4 == 0 and the input is;
+    // output rows likewise with rows. This path has at least one side
+    // misaligned.
+    const bool in_aligned = cols % 4 == 0 && opl::aligned16(input);
+    if (!in_aligned)
+      transpose_vec4u_kernel<false, true><<<grid, block, 0, stream>>>(
+          input, output, rows, cols, vtiles_x, vtiles);
+    else  // only the output side is misaligned
+      transpose_vec4u_kernel<true, false><<<grid, block, 0, stream>>>(
+          input, output, rows, cols, vtiles_x, vtiles);
     return hipGetLastError();
   }
   const int tiles_x = (cols + kTile - 1) / kTile;

@@ -168,8 +168,12 @@ TRANSPOSE_SHAPES = [(37, 65), (64, 96), (65, 37), (1, 1), (1, 1000), (1000, 1),
                     # rows, cols % 4 == 0: the float4 kernel, partial 128-tiles
                     (4, 8), (132, 260), (520, 128), (128, 516), (4, 4096), (1024, 4),
                     # >= 64 tiles of 128x128 at any shape (or offset 1): 16-byte
-                    # accesses at 4-byte alignment, element-wise edge float4s
-                    (1030, 1031), (2049, 1027), (1000, 1000)]
+                    # accesses at 4-byte alignment, element-wise edge float4s;
+                    # misaligned input rows (cached loads) ...
+                    (1030, 1031), (2049, 1027), (1000, 1000),
+                    # ... or, at offset 0, aligned input rows and misaligned
+                    # output rows (cached stores)
+                    (1027, 2048), (4097, 4096)]
 
 
 @pytest.mark.parametrize("shape", TRANSPOSE_SHAPES)
