@@ -292,12 +292,32 @@ class Rowwise:
         assert rc == 0, rc
 
 
-def time_region(torch, launch, launches):
+# Launches longer than this keep the GPU busy up to the timed region
+# instead of queueing behind a spin kernel (see lead_in).
+LONG_LAUNCH_MS = 0.05
+
+
+def lead_in(torch, launch, hot: bool) -> None:
+    """What precedes a timed region. Microsecond launches queue behind a
+    spin kernel, so the host has enqueued all of them before the GPU
+    reaches the first. Long launches (`hot`) are preceded by three untimed
+    launches of their own instead: a near-idle 30 ms spin lets the clocks
+    drop, and the first ~20 ms of matrix-core work after it ran ~12% slower
+    than steady state (GEMM fp16 8192^3: 1.031 ms mean after a spin against
+    0.915 ms per dispatch in the kernel trace)."""
+    if hot:
+        for i in range(3):
+            launch(i)
+    else:
+        spin(torch)
+
+
+def time_region(torch, launch, launches, hot: bool = False):
     """Average duration (ms) of `launch(i)` over `launches` back-to-back launches,
     timed with one pair of HIP events on the launch stream."""
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    spin(torch)
+    lead_in(torch, launch, hot)
     start.record()
     for i in range(launches):
         launch(i)
@@ -312,7 +332,8 @@ WARM_SECONDS = 0.15  # untimed launches before each timed region
 def warm_up(torch, launch, min_launches):
     """Untimed launches: at least `min_launches` and at least WARM_SECONDS of
     wall time, so the timed region starts at the clocks the GPU settles at
-    under this load rather than during its ramp."""
+    under this load rather than during its ramp. Returns the mean wall time
+    per launch (ms)."""
     i, t0 = 0, time.perf_counter()
     while i < min_launches or time.perf_counter() - t0 < WARM_SECONDS:
         launch(i)
@@ -320,13 +341,13 @@ def warm_up(torch, launch, min_launches):
         if i % 16 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
-    return i
+    return (time.perf_counter() - t0) * 1e3 / i
 
 
 GROUP = 8  # launches per group in group_means_ms
 
 
-def group_means_ms(torch, launch, launches):
+def group_means_ms(torch, launch, launches, hot: bool = False):
     """Mean duration (ms) per launch of consecutive groups of GROUP
     back-to-back launches, with one HIP event between groups only. An event
     after every launch drains the queue each time and adds about 2.7 us to
@@ -336,7 +357,7 @@ def group_means_ms(torch, launch, launches):
     groups = max(1, launches // GROUP)
     torch.cuda.synchronize()
     events = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
-    spin(torch)
+    lead_in(torch, launch, hot)
     events[0].record()
     i = 0
     for g in range(groups):
@@ -356,9 +377,9 @@ def time_launches(torch, launch, steps, warmup):
     * ms_median, ms_min, ms_p90: the distribution of group_means_ms over
       max(steps, 8 * GROUP) further launches. The per-dispatch distribution
       (no events at all) is in the kernel-trace profiles."""
-    warm_up(torch, launch, warmup)
-    mean = time_region(torch, launch, steps)
-    d = sorted(group_means_ms(torch, launch, max(steps, 8 * GROUP)))
+    hot = warm_up(torch, launch, warmup) > LONG_LAUNCH_MS
+    mean = time_region(torch, launch, steps, hot)
+    d = sorted(group_means_ms(torch, launch, max(steps, 8 * GROUP), hot))
     p90 = d[min(len(d) - 1, int(round(0.9 * (len(d) - 1))))]
     return {"ms_median": float(np.median(d)), "ms_min": d[0], "ms_p90": p90, "ms_mean": mean,
             "launches": steps, "groups": len(d)}
