@@ -3,8 +3,8 @@
 Every entry point whose launch sequence uses library scratch is called here
 through the C ABI (ctypes releases the GIL, so both threads are inside the
 library together):
-  * reduce_sum_f32 over 1,000,003 values (one partial per workgroup, arrival
-    counter);
+  * reduce_sum_f32 over 1,000,003 values (one fp64 partial per workgroup,
+    then the combine kernel);
   * gemm_f16 1 x 4096 x 4096 (decode GEMM, split-K partials + split sum);
   * gemm_f16 1000^3 (K and N not multiples of the fast kernel's steps:
     zero-padded operand copies, then the product);
