@@ -580,7 +580,6 @@ namespace dma {
 typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
 #define OPL_LDS __attribute__((address_space(3)))
 
-constexpr int kKeys = 64;
 constexpr int kXcds = 8;
 // Grids of fewer query blocks than this split each block's keys in two:
 // below 256 (a CU each) any grid gains; causal grids gain up to 384 blocks,
@@ -591,12 +590,19 @@ constexpr int kXcds = 8;
 // 85.0, causal 61.0 vs 63.6; B4 H32 S8192 causal 2238 vs 2408.
 constexpr long long kSplitKeysBelow = 256;
 constexpr long long kSplitKeysBelowCausal = 512;
-// Grids of at most this many 128-row query blocks run 64-row blocks (two
-// groups of two wavefronts), so that twice as many CUs share the work.
-// Measured on MI355X (us, 128- vs 64-row blocks, keys split in both): B1
-// H12 S1024 20.6 vs 17.6 (causal 20.6 vs 17.5); B1 H8 S2048 34.0 vs 30.0;
-// B1 H4 S512 causal 13.2 vs 10.7; past 128 blocks the 64-row grid needs
-// more than one workgroup per CU: B1 H12 S2048 (192) 35.5 vs 55.3.
+// Grids of at most this many 128-row query blocks run 64-row blocks, so
+// that twice as many CUs share the work. Measured on MI355X (us, 128- vs
+// 64-row blocks, two key groups in both): B1 H12 S1024 20.6 vs 17.6
+// (causal 20.6 vs 17.5); B1 H8 S2048 34.0 vs 30.0; B1 H4 S512 causal 13.2
+// vs 10.7; past 128 blocks the 64-row grid needs more than one workgroup
+// per CU: B1 H12 S2048 (192) 35.5 vs 55.3.
+// At D = 128 these grids split keys four ways (four groups of two
+// wavefronts on 32-key tiles, two wavefronts per SIMD instead of one), so
+// one wavefront's exponentials overlap another's MFMAs. Measured on MI355X
+// (us, two groups on 64-key tiles vs four on 32-key tiles, inputs cycling
+// past the Infinity Cache): B1 H12 S1024 20.5 vs 19.4 (causal 20.6 vs
+// 17.9); B1 H8 S2048 35.4 vs 31.7 (causal 34.6 vs 27.3); B1 H4 S512 11.0
+// vs 11.4 (causal 11.2 vs 11.5).
 constexpr long long kHalfRowsUpTo = 128;
 // D = 64 workgroups hold 64 KiB of LDS (two per CU), so 64-row blocks pay
 // off on larger grids. Measured (us, 128- vs 64-row blocks): B1 H32 S1024
@@ -612,11 +618,11 @@ static_assert(kHalfRowsUpToD64 >= kSplitKeysBelow - 1 &&
 // Headroom (log2 units) the running row max may lag the true max by.
 constexpr float kLazyLog2 = 8.0f;
 
-template <int D>
+template <int D, int kTileKeys>
 struct Layout {
   static constexpr int kRowBytes = D * 2;
   static constexpr int kChunks = kRowBytes / 16;
-  static constexpr int kTile = kKeys * kRowBytes;  // one K or V tile
+  static constexpr int kTile = kTileKeys * kRowBytes;  // one K or V tile
   static constexpr int kStage = 2 * kTile;
   static constexpr int kSteps = D / 16;  // QK^T k-steps
   static constexpr int kDTiles = D / 32;
@@ -628,33 +634,42 @@ struct Layout {
   }
 };
 
-// kGroups = 2 (small grids): two groups of kW wavefronts share the
-// workgroup's query rows and split its key tiles, group 0 the first half
-// and group 1 the rest, each with its own K/V stages; at the end group 1
-// hands its (O, max, sum) to group 0 through LDS, which merges them. A
-// workgroup then holds 128 KiB of LDS (a CU) and each wavefront walks half
-// the keys.
+// kGroups > 1 (small grids): kGroups groups of kW wavefronts share the
+// workgroup's query rows and split its key tiles into contiguous ranges,
+// each group with its own K/V stages; at the end groups 1.. hand their
+// (O, max, sum) to group 0 through LDS, which merges them in group order.
 // kW = wavefronts per group, 32 query rows each: 4 (128-row blocks), or 2
 // (64-row blocks) for the smallest grids, whose 128-row blocks would leave
-// CUs idle: twice the workgroups, one wavefront per SIMD.
-// The 128 KiB of LDS of a D = 128 workgroup fill a CU: with kW = 2 that is
-// one wavefront per SIMD, otherwise two.
-template <int D, int kGroups, int kW>
+// CUs idle.
+// kTileKeys = keys per K/V tile: 64 (two 32-key halves per tile), or 32,
+// which halves the stages so that four groups fit the LDS of two.
+// A D = 128 workgroup with two groups and 64-key tiles, or four groups and
+// 32-key tiles, holds 128 KiB of LDS (a CU): with kW = 2 that is one or two
+// wavefronts per SIMD. The other instances run two wavefronts per SIMD.
+// Two K/V stages per group: the copies of tile t + 1 are issued while tile t
+// is processed. Rings of three and four 32-key stages per group (copies
+// issued two or three tiles ahead, partial vmcnt waits, bare barriers)
+// measured no faster on small grids (B1 H12 S1024: 20.9 us for both
+// against 20.5 us for two 64-key stages), so the tile loop is not waiting
+// on its copies; four groups, two wavefronts per SIMD, are what helps.
+template <int D, int kGroups, int kW, int kTileKeys>
 __global__ __launch_bounds__(kW * opl::kWaveSize * kGroups)
-__attribute__((amdgpu_waves_per_eu(D == 128 && kW == 2 ? 1 : 2, 2)))
+__attribute__((amdgpu_waves_per_eu(D == 128 && kW == 2 && kGroups == 2 ? 1 : 2, 2)))
 void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
                               const _Float16* __restrict__ K,
                               const _Float16* __restrict__ V,
                               float* __restrict__ O, int BH, int S, int causal,
                               float score_scale_log2) {
-  using L = Layout<D>;
-  static_assert(kGroups == 1 || kGroups == 2, "one or two key groups");
+  using L = Layout<D, kTileKeys>;
+  static_assert(kGroups == 1 || kGroups == 2 || kGroups == 4, "1, 2 or 4 key groups");
   static_assert(kW == 2 || kW == 4, "2 or 4 wavefronts per group");
+  static_assert(kTileKeys == 32 || kTileKeys == 64, "32- or 64-key tiles");
   constexpr int kRows = kW * kRowsPerWave;  // query rows per workgroup
   // 16-byte copies per lane and tile: the group's lanes share each tile
   constexpr int kCopies = L::kTile / 16 / (kW * opl::kWaveSize);
-  __shared__ __attribute__((aligned(1024))) unsigned char stage0[kGroups * L::kStage];
-  __shared__ __attribute__((aligned(1024))) unsigned char stage1[kGroups * L::kStage];
+  constexpr int kArray = kGroups * L::kStage;  // bytes of each stage array
+  __shared__ __attribute__((aligned(1024))) unsigned char stage0[kArray];
+  __shared__ __attribute__((aligned(1024))) unsigned char stage1[kArray];
 
   // Work item w = (head, query block) in head-major order, heaviest query
   // block first within a head. Workgroups are dealt to the 8 XCDs
@@ -760,26 +775,27 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   float move_above = -INFINITY;
   const float inv_scale = 1.0f / score_scale_log2;
   const int visible_end = causal ? min(S, q0 + kRows) : S;
-  const int tiles = (visible_end + kKeys - 1) / kKeys;
-  // This group's tiles [t_begin, t_begin + t_count); both groups run
-  // `iters` iterations so that they meet at every barrier.
-  const int first_half = (tiles + 1) / 2;
-  const int t_begin = group == 0 ? 0 : first_half;
-  const int t_count = kGroups == 1 ? tiles : (group == 0 ? first_half : tiles - first_half);
-  const int iters = kGroups == 1 ? tiles : first_half;
+  const int tiles = (visible_end + kTileKeys - 1) / kTileKeys;
+  // This group's tiles [t_begin, t_begin + t_count), a contiguous range of
+  // at most `iters`; every group runs `iters` iterations so that all meet
+  // at every barrier.
+  const int iters = (tiles + kGroups - 1) / kGroups;
+  const int t_begin = group * iters;
+  const int t_count = kGroups == 1 ? tiles : max(0, min(iters, tiles - t_begin));
 
   auto tile = [&](const unsigned char* cur, unsigned char* nxt, int i) {
-    const int key0 = (t_begin + i) * kKeys;
-    if (i + 1 < t_count) issue(nxt, key0 + kKeys);
+    const int key0 = (t_begin + i) * kTileKeys;
+    if (i + 1 < t_count) issue(nxt, key0 + kTileKeys);
     __builtin_amdgcn_sched_barrier(0);
     if ((kGroups == 1 || i < t_count) &&
         (!causal || key0 <= wave_row0 + kRowsPerWave - 1)) {
-      // The tile is processed as two 32-key halves. Lazy rescaling (below)
-      // lets half 1 be exponentiated against the running max before its
-      // own max is checked (it is recomputed in the rare case the max must
-      // move), so one basic block holds the scores of half 1, the P.V
+      // A 64-key tile is processed as two 32-key halves. Lazy rescaling
+      // (below) lets half 1 be exponentiated against the running max before
+      // its own max is checked (it is recomputed in the rare case the max
+      // must move), so one basic block holds the scores of half 1, the P.V
       // product of half 0 (matrix cores) and the exponentials of both
-      // halves (vector ALUs), and the scheduler can interleave them.
+      // halves (vector ALUs), and the scheduler can interleave them. A
+      // 32-key tile is one such half.
       auto scores = [&](int kb) {
         floatx16 s;
 #pragma unroll
@@ -874,21 +890,26 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
         if constexpr (kMasked) mask(s0, 0);
         const float c0 = lane_max(s0);
         if (needs_move(c0)) move_max(c0);
-        floatx16 s1 = scores(1);
-        row_sum += exponentiate(s0, p0);
-        accumulate(0, p0);
-        if constexpr (kMasked) mask(s1, 1);
-        const float c1 = lane_max(s1);
-        float ps1 = exponentiate(s1, p1);
-        if (needs_move(c1)) {
-          move_max(c1);  // after P.V of half 0, which used the old max
-          ps1 = exponentiate(s1, p1);
+        if constexpr (kTileKeys == 32) {
+          row_sum += exponentiate(s0, p0);
+          accumulate(0, p0);
+        } else {
+          floatx16 s1 = scores(1);
+          row_sum += exponentiate(s0, p0);
+          accumulate(0, p0);
+          if constexpr (kMasked) mask(s1, 1);
+          const float c1 = lane_max(s1);
+          float ps1 = exponentiate(s1, p1);
+          if (needs_move(c1)) {
+            move_max(c1);  // after P.V of half 0, which used the old max
+            ps1 = exponentiate(s1, p1);
+          }
+          row_sum += ps1;
+          accumulate(1, p1);
         }
-        row_sum += ps1;
-        accumulate(1, p1);
       };
       // Only tiles crossing the diagonal are masked (a wave-uniform test).
-      if (causal && key0 + kKeys - 1 > wave_row0)
+      if (causal && key0 + kTileKeys - 1 > wave_row0)
         body(std::true_type{});
       else
         body(std::false_type{});
@@ -897,7 +918,7 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     __syncthreads();
   };
 
-  if (t_count > 0) issue(st0, t_begin * kKeys);
+  if (t_count > 0) issue(st0, t_begin * kTileKeys);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   int i = 0;
@@ -907,40 +928,53 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   }
   if (i < iters) tile(st0, st1, i);
 
-  if constexpr (kGroups == 2) {
-    // Every tile of both groups is done (the last iteration ended with a
-    // barrier and issued no copy), so the stages are free. Group 1's
-    // wavefront w hands its state to group 0's wavefront w, which holds the
-    // same rows: O in stage0 (64 values per lane, lane-contiguous so the
-    // accesses are conflict-free), max and sum in stage1.
-    float* xo = reinterpret_cast<float*>(stage0);
-    float* xs = reinterpret_cast<float*>(stage1);
-    const int slot = wave * opl::kWaveSize + lane;
+  if constexpr (kGroups > 1) {
+    // Every tile of every group is done (the last iteration ended with a
+    // barrier and issued no copy), so the stages are free. Wavefront w of
+    // group g > 0 hands its state to wavefront w of group 0, which holds
+    // the same rows: O in region g - 1 (64 values per lane, lane-contiguous
+    // so the accesses are conflict-free), max and sum at the end of stage1.
+    // The exchange space is stage0 followed by stage1.
     constexpr int kSlots = kW * opl::kWaveSize;
-    static_assert(L::kDTiles * 16 * kSlots * 4 <= 2 * L::kStage, "O exchange fits stage0");
-    if (group == 1) {
+    constexpr int kOBytes = L::kDTiles * 16 * kSlots * 4;
+    constexpr int kMLBytes = (kGroups - 1) * 2 * kSlots * 4;
+    static_assert(kArray % kOBytes == 0, "no O region straddles the two arrays");
+    static_assert(kMLBytes <= kArray && (kGroups - 1) * kOBytes <= 2 * kArray - kMLBytes,
+                  "the exchange fits the stages");
+    auto region = [&](int byte) {
+      return reinterpret_cast<float*>(byte < kArray ? stage0 + byte : stage1 + (byte - kArray));
+    };
+    float* const xs = reinterpret_cast<float*>(stage1 + kArray - kMLBytes);
+    const int slot = wave * opl::kWaveSize + lane;
+    if (group > 0) {
+      float* const xo = region((group - 1) * kOBytes);
 #pragma unroll
       for (int dt = 0; dt < L::kDTiles; ++dt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) xo[(dt * 16 + e) * kSlots + slot] = o[dt][e];
-      xs[slot] = row_max;
-      xs[kSlots + slot] = row_sum;
+      xs[(group - 1) * 2 * kSlots + slot] = row_max;
+      xs[(group - 1) * 2 * kSlots + kSlots + slot] = row_sum;
     }
     __syncthreads();
-    if (group == 1) return;
-    // Both halves' p were taken relative to their own running max (log2
-    // units); a half that saw no visible key has max -FLT_MAX, sum 0, O 0.
-    const float m1 = xs[slot];
-    const float l1 = xs[kSlots + slot];
-    const float m = fmaxf(row_max, m1);
-    const float a0 = opl::fast_exp2(row_max - m);
-    const float a1 = opl::fast_exp2(m1 - m);
-    row_sum = row_sum * a0 + l1 * a1;
+    if (group > 0) return;
+    // Each group's p were taken relative to its own running max (log2
+    // units); a group that saw no visible key has max -FLT_MAX, sum 0, O 0.
 #pragma unroll
-    for (int dt = 0; dt < L::kDTiles; ++dt)
+    for (int r = 1; r < kGroups; ++r) {
+      const float* const xo = region((r - 1) * kOBytes);
+      const float m1 = xs[(r - 1) * 2 * kSlots + slot];
+      const float l1 = xs[(r - 1) * 2 * kSlots + kSlots + slot];
+      const float m = fmaxf(row_max, m1);
+      const float a0 = opl::fast_exp2(row_max - m);
+      const float a1 = opl::fast_exp2(m1 - m);
+      row_max = m;
+      row_sum = row_sum * a0 + l1 * a1;
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        o[dt][e] = o[dt][e] * a0 + xo[(dt * 16 + e) * kSlots + slot] * a1;
+      for (int dt = 0; dt < L::kDTiles; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          o[dt][e] = o[dt][e] * a0 + xo[(dt * 16 + e) * kSlots + slot] * a1;
+    }
   }
 
   const float inv = 1.0f / opl::sum_lane_xor32(row_sum);
@@ -992,8 +1026,8 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
       const float scale =
           1.4426950408889634f / sqrtf(static_cast<float>(head_dim));
       // Grids too small to fill the CUs split each query block's keys
-      // between two groups of wavefronts in the workgroup; the smallest
-      // also halve the query block.
+      // between groups of wavefronts in the workgroup; the smallest also
+      // halve the query block, and at D = 128 split its keys four ways.
       const long long half_up_to =
           head_dim == 128 ? dma::kHalfRowsUpTo
                           : (causal ? dma::kHalfRowsUpToD64Causal : dma::kHalfRowsUpToD64);
@@ -1004,24 +1038,26 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
       // a multiple of 8 workgroups, one contiguous range of work per XCD
       const long long padded = (wgs + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
       const dim3 grid(static_cast<unsigned>(padded));
-      const dim3 block(half_rows || !split ? kThreads : 2 * kThreads);
       if (head_dim == 128) {
+        // 64-row blocks x 4 groups / 128-row blocks x 2 groups: 8 wavefronts
+        const dim3 block(split ? 2 * kThreads : kThreads);
         if (half_rows)
-          dma::attention_f16_dma_kernel<128, 2, 2><<<grid, block, 0, stream>>>(
+          dma::attention_f16_dma_kernel<128, 4, 2, 32><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else if (split)
-          dma::attention_f16_dma_kernel<128, 2, 4><<<grid, block, 0, stream>>>(
+          dma::attention_f16_dma_kernel<128, 2, 4, 64><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else
-          dma::attention_f16_dma_kernel<128, 1, 4><<<grid, block, 0, stream>>>(
+          dma::attention_f16_dma_kernel<128, 1, 4, 64><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
       } else {
-        // (split implies half_rows at D = 64)
+        // (split implies half_rows at D = 64; 4 wavefronts either way)
+        const dim3 block(kThreads);
         if (half_rows)
-          dma::attention_f16_dma_kernel<64, 2, 2><<<grid, block, 0, stream>>>(
+          dma::attention_f16_dma_kernel<64, 2, 2, 64><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else
-          dma::attention_f16_dma_kernel<64, 1, 4><<<grid, block, 0, stream>>>(
+          dma::attention_f16_dma_kernel<64, 1, 4, 64><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
       }
       return hipGetLastError();
