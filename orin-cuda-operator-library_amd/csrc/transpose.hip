@@ -3,7 +3,7 @@
 // Reference: operatorlib::transpose_f32 (src/transpose.cu:38-47) with a
 // 32x33 padded shared tile and 32x8 thread blocks sized for 32-lane warps.
 //
-// MI355X design, two kernels:
+// MI355X design, four kernels:
 //   * transpose_vec4_kernel (rows and cols multiples of 4, 16-byte aligned
 //     buffers): a 128x128 fp32 tile per 512-thread workgroup, moved with
 //     16-byte loads and stores in both directions. The 64 KiB tile sits in
@@ -11,14 +11,18 @@
 //     float4) and its 4-row column gathers for the output float4s hit
 //     distinct banks. Long 512-byte row segments on both sides keep HBM
 //     streaming at full rate.
-//   * transpose_vec4u_kernel (any other shape or alignment of at least 64
-//     such tiles, e.g. 4095x4097): the same 128x128 tiles with 16-byte
-//     accesses at 4-byte alignment, float4s crossing the matrix edge moved
-//     element by element, and cache hints chosen by which side is
-//     misaligned (see vec4u_tile). Measured on MI355X against the 4-byte
-//     kernel below (us, both hints non-temporal): 4095x4097 42.3 -> 36.6,
-//     4097x4095 35.9 -> 33.9, 4096x4096 one element off alignment 41.1 ->
-//     36.0, 8191x8193 157.3 -> 142.5.
+//   * transpose_window_kernel (output rows not 16-byte aligned, at least 64
+//     128x128 tiles' worth, e.g. 4095x4097): aligned float4 windows on both
+//     sides, each output row segment starting on a 128-byte line (described
+//     before it).
+//   * transpose_vec4u_kernel (only the input rows misaligned, e.g.
+//     4096x4095): the 128x128 tiles with 16-byte accesses at 4-byte
+//     alignment, float4s crossing the matrix edge moved element by element,
+//     cached loads and non-temporal stores (see vec4u_tile). Measured on
+//     MI355X against the 4-byte kernel below (us, both hints
+//     non-temporal): 4095x4097 42.3 -> 36.6, 4097x4095 35.9 -> 33.9,
+//     4096x4096 one element off alignment 41.1 -> 36.0, 8191x8193 157.3 ->
+//     142.5.
 //   * transpose_tile_kernel (smaller grids of any shape / alignment): a
 //     64x64 tile per 512-thread workgroup (8 wavefronts, 8 rows each)
 //     through a 64x65 LDS array; a wavefront reads one 256-byte input row
@@ -180,9 +184,11 @@ constexpr long long kUnalignedMinTiles = 64;
 //     142.61 -> 134.29.
 // Banding the tiles by XCD, so that tiles sharing a boundary line share an
 // L2, cut FETCH_SIZE at 4095x4097 from 1.27x to 1.00x of the input bytes
-// without changing the time (36.75 us): the misaligned 16-byte accesses
-// themselves, not re-fetched lines, set the cost. Coalesced 4-byte stores
-// for the misaligned output rows were slower (37.66 us).
+// without changing the time (36.75 us): re-fetched input lines do not set
+// the cost. Coalesced 4-byte stores for the misaligned output rows were
+// slower (37.66 us). Output rows misaligned now go to
+// transpose_window_kernel; this kernel keeps cached loads and
+// non-temporal stores for the input-misaligned case.
 template <bool kFull, bool kLoadNT, bool kStoreNT>
 __device__ __forceinline__ void vec4u_tile(const float* __restrict__ input,
                                            float* __restrict__ output, int rows,
@@ -255,6 +261,148 @@ __global__ __launch_bounds__(kThreads) void transpose_vec4u_kernel(
   }
 }
 
+// Line-window transpose, for output rows that are not 16-byte aligned
+// (rows % 4 != 0 or an unaligned output): every store writes whole,
+// aligned 16-byte chunks, and each output row segment a tile writes starts
+// on a 128-byte line, so no line is written partly by two tiles except
+// where an output row itself begins or ends inside a line.
+//   * A tile is kWinCols output rows (input columns col0 ..) by kWinRows
+//     output columns (input rows row0 ..). Output row c takes output
+//     columns [row0 - d, row0 + kWinRows - d), d = (flat index of (c,
+//     row0)) mod 32 — so the windows of consecutive tiles partition the
+//     row, each starting on a line — and the last row block runs to `rows`
+//     (up to kWinHalo more columns).
+//   * The tile therefore needs input rows row0 - 31 .. row0 + kWinRows - 1
+//     (a 31-row halo, read again from L2 by the tile above). Each input
+//     row r is loaded as aligned float4s from column col0 - a(r), a(r) =
+//     (flat index of (r, col0)) mod 4: kWinCols / 4 + 1 of them.
+// Measured on MI355X against transpose_vec4u_kernel (us; inputs cycling
+// through 1 GiB): 4095x4097 35.2 -> 29.7, 4097x4095 32.0 -> 27.7, 8191x8193
+// 134.3 -> 105.8, 4095x4096 29.3 -> 29.2, 1000x1000 5.5 -> 4.6. Where the
+// output rows are aligned and only the input rows are not (4096x4095),
+// transpose_vec4u_kernel stays faster (28.0 vs 32.4) and is kept.
+// 16-byte output windows (a 3-row halo) gained nothing (4095x4097 35.0):
+// the partial lines, not the unaligned float4s, cost the time. Tiles of 128
+// output rows (85 KiB of LDS, one workgroup per CU) took 31.3, 256-column
+// tiles 31.7.
+constexpr int kWinAlign = 32;                          // floats per 128-byte line
+constexpr int kWinHalo = kWinAlign - 1;
+constexpr int kWinCols = 64;                           // output rows per tile
+constexpr int kWinRows = 128;                          // output columns per tile
+constexpr int kWinThreads = 1024;
+constexpr int kWinLdsRows = kWinRows + kWinHalo;       // 159 input rows
+constexpr int kWinChunks = kWinCols / 4 + 1;           // 17 float4 per input row
+constexpr int kWinPitch = 4 * kWinChunks + 1;          // 69 floats
+constexpr int kWinLoads = (kWinLdsRows * kWinChunks + kWinThreads - 1) / kWinThreads;  // 3
+constexpr int kWinStores = kWinCols * (kWinRows / 4) / kWinThreads;                    // 2
+constexpr int kWinExtra = kWinAlign / 4;  // chunks past kWinRows, last row block
+static_assert(kWinCols * (kWinRows / 4) % kWinThreads == 0, "whole store passes");
+
+template <bool kFull>
+__device__ __forceinline__ void window_tile(const float* __restrict__ input,
+                                            float* __restrict__ output, int rows,
+                                            int cols, long long total, int row0,
+                                            int col0, bool last_r, int off_in,
+                                            int off_out, float* lds) {
+  const int cols4 = cols & 3;
+  const int rows32 = rows & (kWinAlign - 1);
+  // LDS row i = input row row0 - kWinHalo + i from column col0 - a(r).
+  float4v v[kWinLoads];
+#pragma unroll
+  for (int n = 0; n < kWinLoads; ++n) {
+    const int q = static_cast<int>(threadIdx.x) + kWinThreads * n;
+    const int i = q / kWinChunks;
+    const int k = q - i * kWinChunks;
+    const int r = row0 - kWinHalo + i;
+    if (q < kWinLdsRows * kWinChunks && (kFull || (r >= 0 && r < rows))) {
+      const int a = ((r & 3) * cols4 + off_in) & 3;
+      const long long f = static_cast<long long>(r) * cols + col0 - a + 4 * k;
+      if (kFull || (f >= 0 && f + 4 <= total)) {
+        // cached: the halo rows are read again by the tile below
+        v[n] = *reinterpret_cast<const float4v*>(input + f);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[n][j] = f + j >= 0 && f + j < total ? input[f + j] : 0.0f;
+      }
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < kWinLoads; ++n) {
+    const int q = static_cast<int>(threadIdx.x) + kWinThreads * n;
+    if (q < kWinLdsRows * kWinChunks) {
+      const int i = q / kWinChunks;
+      float* d = lds + i * kWinPitch + 4 * (q - i * kWinChunks);
+      d[0] = v[n][0];
+      d[1] = v[n][1];
+      d[2] = v[n][2];
+      d[3] = v[n][3];
+    }
+  }
+  __syncthreads();
+  // Chunk k of output row col0 + o: output columns rs .. rs + 3.
+  auto store_chunk = [&](int o, int k, bool extra) {
+    const int c = col0 + o;
+    if (!kFull && c >= cols) return;
+    const int d = ((c & (kWinAlign - 1)) * rows32 + off_out) & (kWinAlign - 1);
+    const int rs = row0 - d + 4 * k;
+    float4v w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int a = (((j - d) & 3) * cols4 + off_in) & 3;  // a(rs + j)
+      // extra chunks store only rows below row0 + kWinRows (LDS rows that exist)
+      const int i = extra ? min(kWinHalo - d + 4 * k + j, kWinLdsRows - 1)
+                          : kWinHalo - d + 4 * k + j;
+      w[j] = lds[i * kWinPitch + o + a];
+    }
+    float* dst = output + static_cast<long long>(c) * rows + rs;
+    if (!extra && (kFull || (rs >= 0 && rs + 4 <= rows))) {
+      __builtin_nontemporal_store(w, reinterpret_cast<float4v*>(dst));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (rs + j >= 0 && rs + j < rows) dst[j] = w[j];
+    }
+  };
+#pragma unroll
+  for (int n = 0; n < kWinStores; ++n) {
+    const int q = static_cast<int>(threadIdx.x) + kWinThreads * n;
+    store_chunk(q / (kWinRows / 4), q % (kWinRows / 4), false);
+  }
+  if (!kFull && last_r) {
+    for (int q = static_cast<int>(threadIdx.x); q < kWinCols * kWinExtra; q += kWinThreads)
+      store_chunk(q / kWinExtra, kWinRows / 4 + q % kWinExtra, true);
+  }
+}
+
+// off_in / off_out: the buffers' offsets, in floats, past a 16-byte /
+// 128-byte boundary.
+__global__ __launch_bounds__(kWinThreads) void transpose_window_kernel(
+    const float* __restrict__ input, float* __restrict__ output, int rows,
+    int cols, int tiles_x, long long tiles, int off_in, int off_out) {
+  __shared__ float lds[kWinLdsRows * kWinPitch];
+  const long long total = static_cast<long long>(rows) * cols;
+  const int tiles_y = static_cast<int>(tiles / tiles_x);
+  for (long long t = blockIdx.x; t < tiles; t += gridDim.x) {
+    const int ty = static_cast<int>(t / tiles_x);
+    const int tx = static_cast<int>(t % tiles_x);
+    const int row0 = ty * kWinRows;
+    const int col0 = tx * kWinCols;
+    const bool last_r = ty == tiles_y - 1;
+    // interior: the halo exists, not the last row block, a full column
+    // block, every float4 load inside the matrix
+    const bool full = row0 >= kWinHalo && !last_r && col0 + kWinCols <= cols &&
+                      static_cast<long long>(row0 + kWinRows - 1) * cols + col0 +
+                              4 * kWinChunks <= total;
+    if (full)
+      window_tile<true>(input, output, rows, cols, total, row0, col0, last_r, off_in,
+                        off_out, lds);
+    else
+      window_tile<false>(input, output, rows, cols, total, row0, col0, last_r, off_in,
+                         off_out, lds);
+    if (t + gridDim.x < tiles) __syncthreads();  // lds is rewritten next
+  }
+}
+
 }  // namespace
 
 extern "C" int operatorlib_transpose_f32(const float* input, float* output,
@@ -277,19 +425,26 @@ extern "C" int operatorlib_transpose_f32(const float* input, float* output,
   const int vtiles_x = (cols + kVecTile - 1) / kVecTile;
   const long long vtiles =
       static_cast<long long>(vtiles_x) * ((rows + kVecTile - 1) / kVecTile);
-  if (vtiles >= kUnalignedMinTiles) {
-    const int blocks = static_cast<int>(vtiles < kMaxGrid ? vtiles : kMaxGrid);
-    const dim3 grid(blocks), block(kThreads);
-    // Input rows are 16-byte aligned when cols % 4 == 0 and the input is;
-    // output rows likewise with rows. This path has at least one side
+  const std::uintptr_t in_addr = reinterpret_cast<std::uintptr_t>(input);
+  const std::uintptr_t out_addr = reinterpret_cast<std::uintptr_t>(output);
+  if (vtiles >= kUnalignedMinTiles && ((in_addr | out_addr) & 3) == 0) {
+    // Output rows are 16-byte aligned when rows % 4 == 0 and the output is;
+    // input rows likewise with cols. This path has at least one side
     // misaligned.
-    const bool in_aligned = cols % 4 == 0 && opl::aligned16(input);
-    if (!in_aligned)
-      transpose_vec4u_kernel<false, true><<<grid, block, 0, stream>>>(
+    const bool out_aligned = rows % 4 == 0 && opl::aligned16(output);
+    if (out_aligned) {  // only the input rows are misaligned
+      const int blocks = static_cast<int>(vtiles < kMaxGrid ? vtiles : kMaxGrid);
+      transpose_vec4u_kernel<false, true><<<dim3(blocks), dim3(kThreads), 0, stream>>>(
           input, output, rows, cols, vtiles_x, vtiles);
-    else  // only the output side is misaligned
-      transpose_vec4u_kernel<true, false><<<grid, block, 0, stream>>>(
-          input, output, rows, cols, vtiles_x, vtiles);
+    } else {
+      const int wtiles_x = (cols + kWinCols - 1) / kWinCols;
+      const long long wtiles =
+          static_cast<long long>(wtiles_x) * ((rows + kWinRows - 1) / kWinRows);
+      const int blocks = static_cast<int>(wtiles < kMaxGrid ? wtiles : kMaxGrid);
+      transpose_window_kernel<<<dim3(blocks), dim3(kWinThreads), 0, stream>>>(
+          input, output, rows, cols, wtiles_x, wtiles, static_cast<int>((in_addr >> 2) & 3),
+          static_cast<int>((out_addr >> 2) & (kWinAlign - 1)));
+    }
     return hipGetLastError();
   }
   const int tiles_x = (cols + kTile - 1) / kTile;

@@ -185,6 +185,30 @@ def test_transpose_bit_exact(hip, shape, offset):
     assert y.view(np.uint32).tobytes() == ref.view(np.uint32).tobytes()
 
 
+# Output rows not 16-byte aligned (the line-window kernel), at independent
+# input / output phases: offsets in floats past a 16-byte (input) and a
+# 128-byte (output) boundary. Rows 1023 and 1022 leave the last 128-row
+# block 127 / 126 rows, whose windows run past it; (1024, 1000) has aligned
+# row lengths and only a misaligned output base.
+WINDOW_SHAPES = [(1000, 1000), (1023, 1025), (1025, 1023), (1022, 1031), (131, 8000),
+                 (8000, 131), (1024, 1000), (2047, 2049)]
+
+
+@pytest.mark.parametrize("shape", WINDOW_SHAPES)
+@pytest.mark.parametrize("in_off,out_off", [(0, 5), (3, 17), (2, 31), (1, 0)])
+def test_transpose_window_phases(lib, shape, in_off, out_off):
+    x = oracle.uniform(430 + shape[1], shape)
+    rows, cols = shape
+    d = to_device(x, in_off)
+    # the output view starts out_off floats past a 256-byte allocation base
+    out = empty((cols, rows), out_off)
+    check(lib.operatorlib_transpose_f32(ptr(d), ptr(out), rows, cols, stream_handle()),
+          "transpose")
+    torch.cuda.synchronize()
+    y = out.cpu().numpy()
+    assert y.view(np.uint32).tobytes() == oracle.transpose(x).view(np.uint32).tobytes()
+
+
 def test_transpose_pins(hip):
     pins.pin_transpose(hip.transpose)
 
