@@ -13,7 +13,7 @@
 //     streaming at full rate.
 //   * transpose_window_kernel (output rows not 16-byte aligned, at least 64
 //     128x128 tiles' worth, e.g. 4095x4097): aligned float4 windows on both
-//     sides, each output row segment starting on a 128-byte line (described
+//     sides, each output row segment starting on a 64-byte boundary (described
 //     before it).
 //   * transpose_vec4u_kernel (only the input rows misaligned, e.g.
 //     4096x4095): the 128x128 tiles with 16-byte accesses at 4-byte
@@ -261,36 +261,38 @@ __global__ __launch_bounds__(kThreads) void transpose_vec4u_kernel(
   }
 }
 
-// Line-window transpose, for output rows that are not 16-byte aligned
-// (rows % 4 != 0 or an unaligned output): every store writes whole,
-// aligned 16-byte chunks, and each output row segment a tile writes starts
-// on a 128-byte line, so no line is written partly by two tiles except
-// where an output row itself begins or ends inside a line.
+// Window transpose, for output rows that are not 16-byte aligned (rows % 4
+// != 0 or an unaligned output): every store writes whole, aligned 16-byte
+// chunks, and each output row segment a tile writes starts on a 64-byte
+// boundary, so no 64-byte block is written partly by two tiles except
+// where an output row itself begins or ends inside one.
 //   * A tile is kWinCols output rows (input columns col0 ..) by kWinRows
 //     output columns (input rows row0 ..). Output row c takes output
 //     columns [row0 - d, row0 + kWinRows - d), d = (flat index of (c,
-//     row0)) mod 32 — so the windows of consecutive tiles partition the
-//     row, each starting on a line — and the last row block runs to `rows`
-//     (up to kWinHalo more columns).
-//   * The tile therefore needs input rows row0 - 31 .. row0 + kWinRows - 1
-//     (a 31-row halo, read again from L2 by the tile above). Each input
-//     row r is loaded as aligned float4s from column col0 - a(r), a(r) =
-//     (flat index of (r, col0)) mod 4: kWinCols / 4 + 1 of them.
+//     row0)) mod 16 -- so the windows of consecutive tiles partition the
+//     row, each starting on a 64-byte boundary -- and the last row block
+//     runs to `rows` (up to kWinHalo more columns).
+//   * The tile therefore needs input rows row0 - 15 .. row0 + kWinRows - 1
+//     (a 15-row halo, read again by the tile above). Each input row r is
+//     loaded as aligned float4s from column col0 - a(r), a(r) = (flat
+//     index of (r, col0)) mod 4: kWinCols / 4 + 1 of them.
 // Measured on MI355X against transpose_vec4u_kernel (us; inputs cycling
-// through 1 GiB): 4095x4097 35.2 -> 29.7, 4097x4095 32.0 -> 27.7, 8191x8193
-// 134.3 -> 105.8, 4095x4096 29.3 -> 29.2, 1000x1000 5.5 -> 4.6. Where the
-// output rows are aligned and only the input rows are not (4096x4095),
-// transpose_vec4u_kernel stays faster (28.0 vs 32.4) and is kept.
-// 16-byte output windows (a 3-row halo) gained nothing (4095x4097 35.0):
-// the partial lines, not the unaligned float4s, cost the time. Tiles of 128
-// output rows (85 KiB of LDS, one workgroup per CU) took 31.3, 256-column
-// tiles 31.7.
-constexpr int kWinAlign = 32;                          // floats per 128-byte line
+// through 1 GiB; windows on 128-byte lines, a 31-row halo): 4095x4097 35.2
+// -> 29.7, 4097x4095 32.0 -> 27.7, 8191x8193 134.3 -> 105.8, 4095x4096
+// 29.3 -> 29.2, 1000x1000 5.5 -> 4.6. Window alignment (us, 4095x4097 /
+// 8191x8193): 16 bytes 35.0 / 127.8, 32 bytes 30.7 / 111.4, 64 bytes
+// 28.6 / 100.1, 128 bytes 29.7 / 106.0. So partly written 64-byte blocks,
+// not the unaligned float4s, cost the time. Where the output rows are
+// aligned and only the input rows are not (4096x4095),
+// transpose_vec4u_kernel stays faster (28.0 vs 32.4 with 128-byte windows)
+// and is kept. Tiles of 128 output rows (85 KiB of LDS, one workgroup per
+// CU) took 31.3, 256-column tiles 31.7 (128-byte windows).
+constexpr int kWinAlign = 16;                          // floats per 64 bytes
 constexpr int kWinHalo = kWinAlign - 1;
 constexpr int kWinCols = 64;                           // output rows per tile
 constexpr int kWinRows = 128;                          // output columns per tile
 constexpr int kWinThreads = 1024;
-constexpr int kWinLdsRows = kWinRows + kWinHalo;       // 159 input rows
+constexpr int kWinLdsRows = kWinRows + kWinHalo;       // 143 input rows
 constexpr int kWinChunks = kWinCols / 4 + 1;           // 17 float4 per input row
 constexpr int kWinPitch = 4 * kWinChunks + 1;          // 69 floats
 constexpr int kWinLoads = (kWinLdsRows * kWinChunks + kWinThreads - 1) / kWinThreads;  // 3
@@ -305,7 +307,7 @@ __device__ __forceinline__ void window_tile(const float* __restrict__ input,
                                             int col0, bool last_r, int off_in,
                                             int off_out, float* lds) {
   const int cols4 = cols & 3;
-  const int rows32 = rows & (kWinAlign - 1);
+  const int rowsA = rows & (kWinAlign - 1);
   // LDS row i = input row row0 - kWinHalo + i from column col0 - a(r).
   float4v v[kWinLoads];
 #pragma unroll
@@ -343,7 +345,7 @@ __device__ __forceinline__ void window_tile(const float* __restrict__ input,
   auto store_chunk = [&](int o, int k, bool extra) {
     const int c = col0 + o;
     if (!kFull && c >= cols) return;
-    const int d = ((c & (kWinAlign - 1)) * rows32 + off_out) & (kWinAlign - 1);
+    const int d = ((c & (kWinAlign - 1)) * rowsA + off_out) & (kWinAlign - 1);
     const int rs = row0 - d + 4 * k;
     float4v w;
 #pragma unroll
@@ -375,7 +377,7 @@ __device__ __forceinline__ void window_tile(const float* __restrict__ input,
 }
 
 // off_in / off_out: the buffers' offsets, in floats, past a 16-byte /
-// 128-byte boundary.
+// 64-byte boundary.
 __global__ __launch_bounds__(kWinThreads) void transpose_window_kernel(
     const float* __restrict__ input, float* __restrict__ output, int rows,
     int cols, int tiles_x, long long tiles, int off_in, int off_out) {
