@@ -429,7 +429,11 @@ extern "C" int operatorlib_transpose_f32(const float* input, float* output,
       static_cast<long long>(vtiles_x) * ((rows + kVecTile - 1) / kVecTile);
   const std::uintptr_t in_addr = reinterpret_cast<std::uintptr_t>(input);
   const std::uintptr_t out_addr = reinterpret_cast<std::uintptr_t>(output);
-  if (vtiles >= kUnalignedMinTiles && ((in_addr | out_addr) & 3) == 0) {
+  // (the window kernel's row and column indices run up to kWinRows /
+  // kWinCols past the matrix in 32-bit arithmetic)
+  constexpr int kIndexRoom = 0x7fffffff - 2 * kWinRows;
+  if (vtiles >= kUnalignedMinTiles && ((in_addr | out_addr) & 3) == 0 &&
+      rows < kIndexRoom && cols < kIndexRoom) {
     // Output rows are 16-byte aligned when rows % 4 == 0 and the output is;
     // input rows likewise with cols. This path has at least one side
     // misaligned.
