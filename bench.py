@@ -545,6 +545,22 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
                             time_launches(torch, f, reps, 3), peak, extra))
         del da, db, c
 
+    if want("gemm") or want("vendor"):
+        # Not operatorlib: the vendor library on the same shape, timed the
+        # same way (torch.matmul on fp16 -> hipBLASLt, fp32 accumulation,
+        # fp16 C, where operatorlib writes fp32 C).
+        size = 8192
+        gen = torch.Generator(device=dev).manual_seed(26)
+        da = (torch.rand((size, size), device=dev, generator=gen) * 2 - 1).half()
+        db = (torch.rand((size, size), device=dev, generator=gen) * 2 - 1).half()
+        c = torch.empty((size, size), device=dev, dtype=torch.float16)
+        f = lambda i: torch.matmul(da, db, out=c)
+        out.append(fl_entry("vendor: torch.matmul fp16 (hipBLASLt, fp16 C)",
+                            [size, size, size], 2 * size ** 3,
+                            time_launches(torch, f, max(5, min(steps, 20)), 3),
+                            FP16_PEAK_TFLOPS))
+        del da, db, c
+
     # Decode-shaped GEMMs (the reference's M == 1 and M <= 16 configurations):
     # HBM-bound on B, reported in GB/s of algorithmic traffic (A, B, C once).
     for name, m in (("gemm_f32", 1), ("gemm_f32", 16), ("gemm_f16", 1), ("gemm_f16", 16)):
@@ -587,6 +603,19 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         extra = {"dense_convention_TFLOPs": round(dense / (t["ms_mean"] * 1e-3) / 1e12, 2),
                  "causal": causal, "flops_convention": "effective (unmasked)"}
         out.append(fl_entry("attention_f16", list(shape), eff, t, FP16_PEAK_TFLOPS, extra))
+        if (bsz, heads, seq) == (4, 32, 8192) and (want("attention") or want("vendor")):
+            # Not operatorlib: PyTorch's fused SDPA on the same inputs, timed
+            # the same way (flash / memory-efficient kernels only, fp16 O).
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            sdpa = torch.nn.functional.scaled_dot_product_attention
+            try:
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                    g = lambda i: sdpa(qkv[0], qkv[1], qkv[2], is_causal=causal)
+                    t = time_launches(torch, g, reps, 3)
+                out.append(fl_entry("vendor: torch SDPA fp16 (fused, fp16 O)", list(shape), eff,
+                                    t, FP16_PEAK_TFLOPS, {"causal": causal}))
+            except RuntimeError as exc:  # no fused kernel for this build
+                out.append({"op": "vendor: torch SDPA fp16", "skipped": str(exc)[:120]})
         del qkv, o
     # FP32 attention (API coverage; no BASELINE config): the S1024 shape of
     # the FP16 configs, and a shape with enough workgroups to fill the GPU.
