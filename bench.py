@@ -546,20 +546,19 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         del da, db, c
 
     if want("gemm") or want("vendor"):
-        # Not operatorlib: the vendor library on the same shape, timed the
-        # same way (torch.matmul on fp16 -> hipBLASLt, fp32 accumulation,
-        # fp16 C, where operatorlib writes fp32 C).
-        size = 8192
-        gen = torch.Generator(device=dev).manual_seed(26)
-        da = (torch.rand((size, size), device=dev, generator=gen) * 2 - 1).half()
-        db = (torch.rand((size, size), device=dev, generator=gen) * 2 - 1).half()
-        c = torch.empty((size, size), device=dev, dtype=torch.float16)
-        f = lambda i: torch.matmul(da, db, out=c)
-        out.append(fl_entry("vendor: torch.matmul fp16 (hipBLASLt, fp16 C)",
-                            [size, size, size], 2 * size ** 3,
-                            time_launches(torch, f, max(5, min(steps, 20)), 3),
-                            FP16_PEAK_TFLOPS))
-        del da, db, c
+        # Not operatorlib: the vendor library on the same shapes, timed the
+        # same way (torch.mm on fp16 with an fp32 result -> hipBLASLt, fp32
+        # accumulation and fp32 C, as operatorlib computes them).
+        for size in (8192, 4096, 4095):
+            gen = torch.Generator(device=dev).manual_seed(26)
+            da = (torch.rand((size, size), device=dev, generator=gen) * 2 - 1).half()
+            db = (torch.rand((size, size), device=dev, generator=gen) * 2 - 1).half()
+            f = lambda i: torch.mm(da, db, out_dtype=torch.float32)
+            out.append(fl_entry("vendor: torch.mm fp16 -> fp32 C (hipBLASLt)",
+                                [size, size, size], 2 * size ** 3,
+                                time_launches(torch, f, max(5, min(steps, 20)), 3),
+                                FP16_PEAK_TFLOPS))
+            del da, db
 
     # Decode-shaped GEMMs (the reference's M == 1 and M <= 16 configurations):
     # HBM-bound on B, reported in GB/s of algorithmic traffic (A, B, C once).
