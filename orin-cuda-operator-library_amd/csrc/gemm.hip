@@ -421,6 +421,9 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   constexpr int kFM = Cfg::kFM, kFN = Cfg::kFN;
   constexpr int kABytes = Cfg::kABytes, kCopies = Cfg::kCopies;
   constexpr int kBChunks = Cfg::kBChunks;
+  constexpr int kReads = kFM + 2 * kFN;  // LDS read instructions per k16 substep
+  constexpr int kIssues = 2 * kCopies;   // DMA instructions per K step
+  static_assert(kWM == 2, "A fragment offsets assume two wavefront rows");
   __shared__ __attribute__((aligned(1024))) unsigned char stage0[Cfg::kStage];
   __shared__ __attribute__((aligned(1024))) unsigned char stage1[Cfg::kStage];
 
@@ -438,6 +441,7 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   const int wn = wave % kWN;
   const int half = lane / 32;
   const int l32 = lane % 32;
+  const int steps = K / kBK;
 
   // DMA sources: copy j of this thread fills LDS chunk slot
   // (wave * kCopies + j) * 64 + lane of each operand tile. They are byte
@@ -456,52 +460,52 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
     const int col = n0 + 8 * ((lane % kBChunks) ^ swizzle_b(kk));
     b_dma[j] = kk * ldb * 2 + (min(col, ldb - 8) - n0) * 2;
   }
-  // Bytes from each step's base to the end of its operand, capped at the
-  // 32-bit range (every offset above stays far below it).
+  // Bytes from a step's base to the end of its operand, capped at the
+  // 32-bit range (every offset above stays far below it). Steps past the
+  // end get an empty range: their copies read zeros and touch no memory.
   auto span = [](long long bytes) {
     return static_cast<unsigned>(bytes < 0xffffffffLL ? bytes : 0xffffffffLL);
   };
-  auto issue = [&](unsigned char* stage, int k0) {
-    unsigned char* sb = stage + kABytes;
+  const long long a_total = static_cast<long long>(M - m0) * K * 2;
+  const long long b_total = static_cast<long long>(K) * ldb * 2 - 2LL * n0;
+  auto issue = [&](unsigned char* stage, int kstep) {
+    const int k0 = kstep * kBK;
+    const unsigned live = kstep < steps ? ~0u : 0u;
+    const unsigned a_span = span(a_total - 2LL * k0) & live;
+    const unsigned b_span = span(b_total - 2LL * k0 * ldb) & live;
     const _Float16* a_base = A + static_cast<std::size_t>(m0) * K + k0;
     const _Float16* b_base = B + static_cast<std::size_t>(k0) * ldb + n0;
-    const unsigned a_span =
-        span((static_cast<long long>(M - m0) * K - k0) * 2);
-    const unsigned b_span =
-        span((static_cast<long long>(K - k0) * ldb - n0) * 2);
 #pragma unroll
-    for (int j = 0; j < kCopies; ++j)
+    for (int j = 0; j < kCopies; ++j) {
       opl::buffer_copy16_lds(a_base, a_span, stage + (wave * kCopies + j) * 1024,
                              a_dma[j], 0);
-#pragma unroll
-    for (int j = 0; j < kCopies; ++j)
-      opl::buffer_copy16_lds(b_base, b_span, sb + (wave * kCopies + j) * 1024,
+      opl::buffer_copy16_lds(b_base, b_span, stage + kABytes + (wave * kCopies + j) * 1024,
                              b_dma[j], 0);
+    }
   };
 
-  // Fragment byte offsets inside a stage for each of the 4 k16 steps.
-  int a_off[kFM][4];
-#pragma unroll
-  for (int ti = 0; ti < kFM; ++ti) {
-    const int m = wm * (kBM / kWM) + 32 * ti + l32;
+  // Fragment byte offsets inside a stage. A: the swizzle (m >> 1) & 7 of
+  // row m = wm * BM / 2 + 32 ti + l32 does not depend on ti, so one VGPR
+  // per k16 substep s serves every ti (rows 32 apart are 4096 bytes
+  // apart). B: k & 3 = gl / 4 for every s and half-row r, so one VGPR per
+  // tj serves every s and r (16 rows further per s, 4 rows per r).
+  constexpr int kBSubstep = 16 * Cfg::kBRowBytes;
+  unsigned a_lane[4];
+  {
+    const int m = wm * (kBM / kWM) + l32;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      a_off[ti][s] = m * 128 + (((2 * s + half) ^ swizzle_a(m)) * 16);
+      a_lane[s] = m * 128 + (((2 * s + half) ^ swizzle_a(m)) * 16);
   }
   const int group = lane / 16;
   const int gl = lane % 16;
-  int b_off[kFN][4][2];
+  unsigned b_lane[kFN];
 #pragma unroll
-  for (int tj = 0; tj < kFN; ++tj)
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int n = wn * (kBN / kWN) + 32 * tj + 16 * (group % 2) + 4 * (gl % 4);
-        const int k = 16 * s + 8 * (group / 2) + 4 * r + gl / 4;
-        b_off[tj][s][r] = kABytes + k * Cfg::kBRowBytes +
-                          (((n / 8) ^ swizzle_b(k)) * 16) + (n % 8) * 2;
-      }
+  for (int tj = 0; tj < kFN; ++tj) {
+    const int n = wn * (kBN / kWN) + 32 * tj + 16 * (group % 2) + 4 * (gl % 4);
+    const int k = 8 * (group / 2) + gl / 4;
+    b_lane[tj] = kABytes + k * Cfg::kBRowBytes + (((n / 8) ^ swizzle_b(k)) * 16) + (n % 8) * 2;
+  }
 
   floatx16 acc[kFM][kFN];
 #pragma unroll
@@ -513,21 +517,21 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
 
   auto load = [&](const unsigned char* st, int s, Fragments<Cfg>& f) {
 #pragma unroll
-    for (int ti = 0; ti < kFM; ++ti)
-      f.a[ti] = *reinterpret_cast<const half8*>(st + a_off[ti][s]);
+    for (int t = 0; t < (kFM > kFN ? kFM : kFN); ++t) {
+      if (t < kFM) f.a[t] = *reinterpret_cast<const half8*>(st + a_lane[s] + t * 4096);
+      if (t < kFN) {
+        const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s));
+        const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s + kBSubstep / 4));
+        half8 b;
 #pragma unroll
-    for (int tj = 0; tj < kFN; ++tj) {
-      const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-          (OPL_LDS fp16x4*)(st + b_off[tj][s][0]));
-      const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-          (OPL_LDS fp16x4*)(st + b_off[tj][s][1]));
-      half8 b;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        b[e] = lo[e];
-        b[4 + e] = hi[e];
+        for (int e = 0; e < 4; ++e) {
+          b[e] = lo[e];
+          b[4 + e] = hi[e];
+        }
+        f.b[t] = b;
       }
-      f.b[tj] = b;
     }
   };
   auto mma = [&](const Fragments<Cfg>& f) {
@@ -538,39 +542,74 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
         acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
             f.a[ti], f.b[tj], acc[ti][tj], 0, 0, 0);
   };
-
-  const int steps = K / kBK;
-  auto tile = [&](const unsigned char* cur, unsigned char* nxt, int step) {
-    if (step + 1 < steps) issue(nxt, (step + 1) * kBK);
-    __builtin_amdgcn_sched_barrier(0);
-    Fragments<Cfg> f0, f1;
-    load(cur, 0, f0);
-    __builtin_amdgcn_sched_barrier(0);
+  // Scheduling groups for one substep: each MFMA followed by its share of
+  // the LDS reads (the next substep's fragments) and, with_dma, of the DMA
+  // issues, so reads and copies issue in the MFMAs' shadow instead of in a
+  // burst (one of each per MFMA for 256 x 256 tiles, two for 128 x 128).
+  constexpr int kMfmas = kFM * kFN;
+  constexpr int kReadsPer = (kReads + kMfmas - 1) / kMfmas;
+  constexpr int kIssuesPer = (kIssues + kMfmas - 1) / kMfmas;
+  auto interleave = [&](bool with_dma) {
 #pragma unroll
-    for (int s = 0; s < 4; s += 2) {
-      load(cur, s + 1, f1);
-      __builtin_amdgcn_sched_barrier(0);
-      mma(f0);
-      __builtin_amdgcn_sched_barrier(0);
-      if (s + 2 < 4) load(cur, s + 2, f0);
-      __builtin_amdgcn_sched_barrier(0);
-      mma(f1);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < kMfmas; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (i * kReadsPer < kReads)
+        __builtin_amdgcn_sched_group_barrier(0x100, kReadsPer, 0);  // DS read
+      if (with_dma && i * kIssuesPer < kIssues)
+        __builtin_amdgcn_sched_group_barrier(0x010, kIssuesPer, 0);  // VMEM
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this step's reads and the next DMA
-    __syncthreads();
+  };
+  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(0): this wave's LDS reads and
+  // DMA copies complete. The release fence of __syncthreads() does not
+  // wait for the copies, so the wait is explicit and the barrier bare.
+  auto sync_stage = [] {
+    __builtin_amdgcn_s_waitcnt(0x0070);
+    asm volatile("s_barrier" ::: "memory");
+  };
+
+  // Step `step` computes from `cur` (complete); `nxt` holds step + 1 (in
+  // flight). Substeps 0-2 each read the next substep's fragments from
+  // `cur` under their MFMAs. Then every wave has finished reading `cur`
+  // and step + 1 has landed (sync_stage), so substep 3 refills `cur` with
+  // step + 2 and reads the next step's first fragments from `nxt` under
+  // its MFMAs: the barrier never waits on an LDS read.
+  Fragments<Cfg> f0, f1;
+  auto tile = [&](unsigned char* cur, unsigned char* nxt, int step) {
+    load(cur, 1, f1);
+    mma(f0);
+    interleave(false);
+    __builtin_amdgcn_sched_barrier(0);
+    load(cur, 2, f0);
+    mma(f1);
+    interleave(false);
+    __builtin_amdgcn_sched_barrier(0);
+    load(cur, 3, f1);
+    mma(f0);
+    interleave(false);
+    __builtin_amdgcn_sched_barrier(0);
+    sync_stage();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(cur, step + 2);
+    load(nxt, 0, f0);
+    mma(f1);
+    interleave(true);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   issue(stage0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  issue(stage1, 1);
+  sync_stage();
+  load(stage0, 0, f0);
+  __builtin_amdgcn_sched_barrier(0);
   int step = 0;
   for (; step + 1 < steps; step += 2) {
     tile(stage0, stage1, step);
     tile(stage1, stage0, step + 1);
   }
   if (step < steps) tile(stage0, stage1, step);
+  __builtin_amdgcn_s_waitcnt(0);  // the last (empty) copies
 
+  const bool full = m0 + kBM <= M && n0 + kBN <= N;
 #pragma unroll
   for (int ti = 0; ti < kFM; ++ti) {
 #pragma unroll
@@ -580,7 +619,7 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
       for (int e = 0; e < 16; ++e) {
         const int row =
             m0 + wm * (kBM / kWM) + 32 * ti + 8 * (e / 4) + 4 * half + (e % 4);
-        if (row < M && col < N)
+        if (full || (row < M && col < N))
           C[static_cast<std::size_t>(row) * N + col] = acc[ti][tj][e];
       }
     }

@@ -390,6 +390,23 @@ def test_gemm_small_grid_tiles(hip, mnk, dtype):
     assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize("mnk", [(4000, 2600, 1088), (4096, 2560, 64), (1000, 1000, 64),
+                                 (520, 2056, 192)])
+def test_gemm_f16_step_counts(hip, mnk):
+    """fp16 matrix-core tiles over odd numbers of 64-deep K steps (the loop
+    runs steps in pairs), a single step, and ragged last tile rows and
+    columns; both tile sizes (176 and 160 big tiles, then small grids)."""
+    m, n, k = mnk
+    a = oracle.to_f16_bits(oracle.uniform(680 + m, (m, k)))
+    b = oracle.to_f16_bits(oracle.uniform(681 + n, (k, n)))
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(m - 8, m),
+                                     sample_rows(m, 24, 682)]))
+    y = hip.gemm_f16(a, b)
+    ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b), rows)
+    assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    assert np.isfinite(y).all()
+
+
 def test_gemm_padded_then_smaller(hip):
     """The per-stream workspace is reused: a large padded call followed by a
     smaller one (and a larger one, which grows it) must all be right."""
