@@ -360,13 +360,23 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 //     and it keeps 128-byte (A) / 512-byte (B) contiguous global segments;
 //   * two LDS stages in separate arrays (so the compiler can see that the
 //     DMA into one does not alias the reads of the other), the loop unrolled
-//     by two; fragments for step s+1 are read while step s runs on the
-//     matrix cores (sched_barrier keeps that order);
+//     by two. Each 64-deep K step is four k16 substeps; every substep reads
+//     the next substep's fragments under its MFMAs, one LDS read (two for
+//     128 x 128 tiles) after each MFMA (sched_group_barrier). The step's
+//     barrier comes before its last substep: by then every wave has read
+//     its last fragments from the stage and the next stage has landed, so
+//     the last substep's MFMAs cover both the next step's first fragment
+//     reads and the DMA refill of the stage just finished (interleaved the
+//     same way: the copies issued in one burst measured about 2% slower);
+//   * copies of steps past the end read through an empty buffer range
+//     (zeros, no memory access), so every step runs the same code;
 //   * M / N edges: source rows / columns are clamped into the matrix (their
 //     results are never stored), stores are masked.
-// Measured on MI355X (8192^3): 1.01-1.16 PFLOP/s (the lower figures under
-// sustained load), 84-96% of hipBLASLt's fp16 GEMM on the same boxes
-// (1.21 PFLOP/s).
+// Measured on MI355X (median of 8-launch groups): 4096^3 114-117 us, 8192^3
+// 887-910 us (1.20-1.24 PFLOP/s); hipBLASLt with the same fp32 C: 112-116
+// and 827-859 us. The previous schedule (all fragment reads of a substep
+// in one batch, copies issued in a burst at the top of the step, barrier at
+// its end) ran 122 / 925 us, bit-identical output.
 // ---------------------------------------------------------------------------
 
 namespace dma {
