@@ -23,6 +23,8 @@
 #include <cfloat>
 #include <cmath>
 #include <cstddef>
+#include <cstdint>
+#include <type_traits>
 
 #include "common.hpp"
 #include "operatorlib/operatorlib_c.h"
@@ -152,6 +154,105 @@ __global__ __launch_bounds__(opl::kRowBlockThreads) void softmax_two_pass_kernel
   }
 }
 
+// Ragged fp32 rows of up to kTileMaxCols columns (cols % 4 != 0 or
+// unaligned rows) as flat tiles: a workgroup's 4 consecutive rows are one
+// contiguous range of the matrix, moved between HBM and LDS in aligned
+// 16-byte chunks (scalar accesses only for the range's first and last
+// partial chunk), and each wavefront reduces its row out of LDS. Per-row
+// misaligned starts cost the one-row-per-wavefront kernel ~1 us per 4097 x
+// 1023 call (7.6 us against 6.0 aligned); here only every fourth row
+// boundary is a chunk boundary shared with another workgroup. Measured on
+// MI355X (us, cold buffers): 4097 x 1023 7.62 -> 7.06, 8191 x 511 7.99 ->
+// 7.69. 8 rows per workgroup: 7.13 / 6.92; 16: 8.23 / 6.75. fp16 rows and
+// longer rows measured slower this way (4097 x 1023 fp16 4.78 -> 5.64,
+// 2047 x 4095 12.90 -> 13.39: the fp32 tile doubles the fp16 bytes through
+// LDS, and 64 KiB tiles halve the workgroups per CU), so they keep the
+// wavefront kernel. V: columns per lane / 4.
+constexpr int kTileMaxCols = 1024;
+template <int V>
+__global__ __launch_bounds__(opl::kRowWaveThreads) void softmax_tile_kernel(
+    const float* __restrict__ input, float* __restrict__ output, int rows, int cols) {
+  typedef float F4 __attribute__((ext_vector_type(4)));
+  constexpr int kT = opl::kRowWaveThreads;
+  constexpr int kRows = opl::kRowWaveRows;
+  constexpr int kPerLane = 4 * V;  // row elements per lane
+  // kRows rows of up to 64 * kPerLane columns, plus one chunk of lead-in
+  __shared__ __attribute__((aligned(16))) float tile[kRows * opl::kWaveSize * kPerLane + 4];
+  const int t = threadIdx.x;
+  const int r0 = blockIdx.x * kRows;
+  const int nrows = min(kRows, rows - r0);
+  const int n = nrows * cols;  // elements of the range, >= 8
+  const float* in = input + static_cast<std::size_t>(r0) * cols;
+  float* out = output + static_cast<std::size_t>(r0) * cols;
+  // Range element k sits at tile[lead + k]: lead is the range start's
+  // offset from the 16-byte boundary below it, so every aligned chunk of the
+  // range is an aligned 16-byte LDS slot too (output rows share the input's
+  // phase, so the same chunks are aligned there).
+  const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(in) & 15) / 4);
+  const int head = (4 - lead) % 4;  // elements before the first boundary
+  const int body = (n - head) / 4;  // aligned chunks, >= 1
+  const int tail0 = head + 4 * body;
+  // Thread t loads chunks t + kT * j (indices clamped: loads issue back to
+  // back, out-of-range ones are dropped on the LDS write); threads 0 .. head-1
+  // take the head elements, threads 4 .. 4 + (n - tail0) - 1 the tail.
+  const F4* bin = reinterpret_cast<const F4*>(in + head);
+  F4 q[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int c = t + kT * j;
+    q[j] = __builtin_nontemporal_load(bin + (c < body ? c : 0));
+  }
+  const int xc = t < head ? t : (t >= 4 && t - 4 < n - tail0 ? tail0 + t - 4 : -1);
+  const float xv = in[xc >= 0 ? xc : 0];
+  float* const base = tile + lead + head;  // 16-byte aligned
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int c = t + kT * j;
+    if (c < body) *reinterpret_cast<F4*>(base + 4 * c) = q[j];
+  }
+  if (xc >= 0) tile[lead + xc] = xv;
+  __syncthreads();
+  const int w = t / opl::kWaveSize;
+  const int lane = t % opl::kWaveSize;
+  if (w < nrows) {
+    float* const rowp = tile + lead + w * cols;
+    float x[kPerLane];
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+      const int c = lane + opl::kWaveSize * i;
+      x[i] = c < cols ? rowp[c] : -INFINITY;
+    }
+    const float m = opl::wave_reduce<opl::MaxOp>(local_max(x));
+    const float sum = opl::wave_reduce<opl::SumOp>(exp_shift_sum(x, m));
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+      const int c = lane + opl::kWaveSize * i;
+      if (c < cols) rowp[c] = x[i] * inv;
+    }
+  }
+  __syncthreads();
+  F4* const bout = reinterpret_cast<F4*>(out + head);
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int c = t + kT * j;
+    if (c < body)
+      __builtin_nontemporal_store(*reinterpret_cast<const F4*>(base + 4 * c), bout + c);
+  }
+  if (xc >= 0) __builtin_nontemporal_store(tile[lead + xc], out + xc);
+}
+
+template <int V>
+void launch_tile(int v, const float* in, float* out, int rows, int cols,
+                 hipStream_t stream) {
+  if constexpr (4 * V * opl::kWaveSize < kTileMaxCols) {
+    if (v > V) return launch_tile<2 * V>(v, in, out, rows, cols, stream);
+  }
+  const int blocks = (rows + opl::kRowWaveRows - 1) / opl::kRowWaveRows;
+  softmax_tile_kernel<V><<<dim3(blocks), dim3(opl::kRowWaveThreads), 0, stream>>>(
+      in, out, rows, cols);
+}
+
 // Launches the kernel instance whose per-thread count V is the smallest power
 // of two >= v (v comes from pick_row_plan, so it never exceeds MaxV).
 template <typename T, int W, int V, int MaxV>
@@ -200,6 +301,9 @@ int softmax_launch(const T* input, T* output, int rows, int cols,
   switch (plan.path) {
     case opl::RowPath::kWave:
       if (vec) launch_wave<T, E, 1, kWaveMaxV>(plan.per_thread, input, output, rows, cols, stream);
+      else if (ragged && std::is_same<T, float>::value && cols <= kTileMaxCols)
+        launch_tile<1>(plan.per_thread, reinterpret_cast<const float*>(input),
+                       reinterpret_cast<float*>(output), rows, cols, stream);
       else if (ragged) launch_wave<T, 0, 1, kWaveMaxV>(plan.per_thread, input, output, rows, cols, stream);
       else launch_wave<T, 1, 1, 64>(plan.per_thread, input, output, rows, cols, stream);
       break;

@@ -90,7 +90,10 @@ def test_reduce_two_streams(lib):
 
 SOFTMAX_SHAPES = [(19, 128), (17, 1024), (17, 1003), (5, 1), (3, 7), (1, 4096),
                   (7, 4100), (3, 9000), (2, 32768), (2, 40000), (3, 33333),
-                  (4096, 1024), (4097, 1023)]
+                  (4096, 1024), (4097, 1023),
+                  # flat 4-row tiles of ragged rows: one short range, a
+                  # partial last tile, a single row of the minimum length
+                  (4, 9), (6, 1000), (1, 8)]
 
 
 @pytest.mark.parametrize("shape", SOFTMAX_SHAPES)
