@@ -240,6 +240,25 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n,
   *tn = in_group / rows_in_group;
 }
 
+// Grids of whole 16 x 16 blocks of tiles with one workgroup per CU: each
+// round of 256 workgroups (one per CU) takes one 16 x 16 super-tile, and XCD
+// x an 8 x 4 block of it, in column-major order within the block. A round
+// then reads 16 tile rows of A and 16 tile columns of B, where the grouped
+// order above spreads a round over all tile rows (8192 x 8192 tiles of 256:
+// 32 tile rows and 8 tile columns). Measured on MI355X, fp16, us (grouped
+// vs super-tiles): 8192 x 8192 x 4096 500 vs 458, 16384 x 4096 x 4096 486
+// vs 475, 8192^3 910 vs 909, 4096^3 117 vs 117 (the same order there).
+// Needs gridDim.x = tiles_m * tiles_n with tiles_m, tiles_n % 16 == 0.
+__device__ __forceinline__ void super_tile_of_block(int tiles_n, int* tm, int* tn) {
+  const int x = blockIdx.x % kXcds;   // XCD (workgroups are dealt round-robin)
+  const int j = blockIdx.x / kXcds;   // this XCD's j-th workgroup
+  const int round = j / 32;           // 32 workgroups per XCD and round
+  const int q = j % 32;
+  const int super_cols = tiles_n / 16;
+  *tm = (round / super_cols) * 16 + (x / 4) * 8 + q % 8;
+  *tn = (round % super_cols) * 16 + (x % 4) * 4 + q / 8;
+}
+
 template <typename T, bool kVector, typename L = typename LayoutFor<T>::type>
 __global__ __launch_bounds__(L::kThreads)
 __attribute__((amdgpu_waves_per_eu(L::kWavesPerSimd, L::kWavesPerSimd)))
@@ -440,7 +459,11 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   const int tiles_m = (M + kBM - 1) / kBM;
   const int tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
-  tile_of_block(tiles_m, tiles_n, &tm, &tn);
+  // 256 x 256 tiles run one workgroup per CU (128 KiB of LDS)
+  if (kBM == 256 && tiles_m % 16 == 0 && tiles_n % 16 == 0)
+    super_tile_of_block(tiles_n, &tm, &tn);
+  else
+    tile_of_block(tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * kBM;
   const int n0 = tn * kBN;
 
