@@ -223,21 +223,27 @@ struct Stager {
   }
 };
 
-// Maps the launch index to a C tile: first regroups the round-robin XCD
-// dispatch so consecutive tiles land on one XCD, then walks tiles in
-// column-major groups of kGroupM tile-rows.
-__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n,
-                                              int* tm, int* tn) {
-  const int blocks = gridDim.x;
-  int bid = blockIdx.x;
-  if (blocks % kXcds == 0)
-    bid = (bid % kXcds) * (blocks / kXcds) + bid / kXcds;
+// Tile `idx` of the grouped order: column-major groups of kGroupM tile-rows.
+__device__ __forceinline__ void grouped_tile(int idx, int tiles_m, int tiles_n,
+                                             int* tm, int* tn) {
   const int group_size = kGroupM * tiles_n;
-  const int first_m = (bid / group_size) * kGroupM;
+  const int first_m = (idx / group_size) * kGroupM;
   const int rows_in_group = min(tiles_m - first_m, kGroupM);
-  const int in_group = bid % group_size;
+  const int in_group = idx % group_size;
   *tm = first_m + in_group % rows_in_group;
   *tn = in_group / rows_in_group;
+}
+
+// Launch index b of `blocks` -> grouped-order index: regroups the
+// round-robin XCD dispatch so that consecutive tiles land on one XCD.
+__device__ __forceinline__ int xcd_regroup(int b, int blocks) {
+  return blocks % kXcds == 0 ? (b % kXcds) * (blocks / kXcds) + b / kXcds : b;
+}
+
+// Maps the launch index to a C tile: XCD regrouping, then the grouped order.
+__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n,
+                                              int* tm, int* tn) {
+  grouped_tile(xcd_regroup(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
 }
 
 // Grids of whole 16 x 16 blocks of tiles with one workgroup per CU: each
@@ -401,6 +407,18 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 namespace dma {
 
 typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
+
+// Split of a grid's last, partly filled round: launch indices below
+// full_tiles take whole tiles; the `tiles` tiles after them in the grouped
+// order are each cut into `splits` contiguous K ranges, one workgroup per
+// range, written to `partial` ([splits][tiles][BM x BN] fp32) and summed by
+// sum_tail_kernel. splits == 0: no split, one workgroup per tile.
+struct TailSplit {
+  int full_tiles;
+  int tiles;
+  int splits;
+  float* partial;
+};
 #define OPL_LDS __attribute__((address_space(3)))
 
 // C tile configurations. BM x BN per workgroup, WM x WN wavefronts of
@@ -440,11 +458,12 @@ struct Fragments {
   half8 b[Cfg::kFN];
 };
 
-template <typename Cfg>
+template <typename Cfg, bool kTail = false>
 __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
                          const _Float16* __restrict__ B,
-                         float* __restrict__ C, int M, int N, int K, int ldb) {
+                         float* __restrict__ C, int M, int N, int K, int ldb,
+                         TailSplit tail) {
   constexpr int kBM = Cfg::kBM, kBN = Cfg::kBN, kBK = Cfg::kBK;
   constexpr int kWM = Cfg::kWM, kWN = Cfg::kWN;
   constexpr int kFM = Cfg::kFM, kFN = Cfg::kFN;
@@ -459,11 +478,30 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   const int tiles_m = (M + kBM - 1) / kBM;
   const int tiles_n = (N + kBN - 1) / kBN;
   int tm, tn;
-  // 256 x 256 tiles run one workgroup per CU (128 KiB of LDS)
-  if (kBM == 256 && tiles_m % 16 == 0 && tiles_n % 16 == 0)
+  // K steps [kstep0, kstep0 + steps) of the tile; split >= 0: a tail part
+  // (kTail instances only; the others keep kstep0 = 0 at compile time).
+  int kstep0 = 0;
+  int steps = K / kBK;
+  int split = -1, tail_index = 0;
+  if constexpr (kTail) {
+    const int b = blockIdx.x;
+    if (b < tail.full_tiles) {
+      grouped_tile(xcd_regroup(b, tail.full_tiles), tiles_m, tiles_n, &tm, &tn);
+    } else {
+      const int w = b - tail.full_tiles;
+      tail_index = w / tail.splits;
+      split = w % tail.splits;
+      grouped_tile(tail.full_tiles + tail_index, tiles_m, tiles_n, &tm, &tn);
+      const int per = steps / tail.splits, extra = steps % tail.splits;
+      kstep0 = split * per + min(split, extra);
+      steps = per + (split < extra ? 1 : 0);
+    }
+  } else if (kBM == 256 && tiles_m % 16 == 0 && tiles_n % 16 == 0) {
+    // 256 x 256 tiles run one workgroup per CU (128 KiB of LDS)
     super_tile_of_block(tiles_n, &tm, &tn);
-  else
+  } else {
     tile_of_block(tiles_m, tiles_n, &tm, &tn);
+  }
   const int m0 = tm * kBM;
   const int n0 = tn * kBN;
 
@@ -474,7 +512,6 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   const int wn = wave % kWN;
   const int half = lane / 32;
   const int l32 = lane % 32;
-  const int steps = K / kBK;
 
   // DMA sources: copy j of this thread fills LDS chunk slot
   // (wave * kCopies + j) * 64 + lane of each operand tile. They are byte
@@ -499,15 +536,19 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   auto span = [](long long bytes) {
     return static_cast<unsigned>(bytes < 0xffffffffLL ? bytes : 0xffffffffLL);
   };
-  const long long a_total = static_cast<long long>(M - m0) * K * 2;
-  const long long b_total = static_cast<long long>(K) * ldb * 2 - 2LL * n0;
+  // Operand origins of this tile's first K step (kstep0 > 0: a tail part).
+  const _Float16* const a_tile = A + static_cast<std::size_t>(m0) * K + kstep0 * kBK;
+  const _Float16* const b_tile = B + static_cast<std::size_t>(kstep0) * kBK * ldb + n0;
+  const long long a_total = static_cast<long long>(M - m0) * K * 2 - 2LL * kstep0 * kBK;
+  const long long b_total =
+      (static_cast<long long>(K) - static_cast<long long>(kstep0) * kBK) * ldb * 2 - 2LL * n0;
   auto issue = [&](unsigned char* stage, int kstep) {
     const int k0 = kstep * kBK;
     const unsigned live = kstep < steps ? ~0u : 0u;
     const unsigned a_span = span(a_total - 2LL * k0) & live;
     const unsigned b_span = span(b_total - 2LL * k0 * ldb) & live;
-    const _Float16* a_base = A + static_cast<std::size_t>(m0) * K + k0;
-    const _Float16* b_base = B + static_cast<std::size_t>(k0) * ldb + n0;
+    const _Float16* a_base = a_tile + k0;
+    const _Float16* b_base = b_tile + static_cast<std::size_t>(k0) * ldb;
 #pragma unroll
     for (int j = 0; j < kCopies; ++j) {
       opl::buffer_copy16_lds(a_base, a_span, stage + (wave * kCopies + j) * 1024,
@@ -642,21 +683,59 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   if (step < steps) tile(stage0, stage1, step);
   __builtin_amdgcn_s_waitcnt(0);  // the last (empty) copies
 
-  const bool full = m0 + kBM <= M && n0 + kBN <= N;
+  // A tail part writes its whole tile, row-major, to its partial slot;
+  // sum_tail_kernel adds the parts in split order.
+  float* const out = split >= 0
+      ? tail.partial + static_cast<std::size_t>(split * tail.tiles + tail_index) * kBM * kBN
+      : C + static_cast<std::size_t>(m0) * N + n0;
+  const int ldo = split >= 0 ? kBN : N;
+  const int row_end = split >= 0 ? kBM : M - m0;
+  const int col_end = split >= 0 ? kBN : N - n0;
+  const bool full = row_end >= kBM && col_end >= kBN;
 #pragma unroll
   for (int ti = 0; ti < kFM; ++ti) {
 #pragma unroll
     for (int tj = 0; tj < kFN; ++tj) {
-      const int col = n0 + wn * (kBN / kWN) + 32 * tj + l32;
+      const int col = wn * (kBN / kWN) + 32 * tj + l32;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int row =
-            m0 + wm * (kBM / kWM) + 32 * ti + 8 * (e / 4) + 4 * half + (e % 4);
-        if (full || (row < M && col < N))
-          C[static_cast<std::size_t>(row) * N + col] = acc[ti][tj][e];
+        const int row = wm * (kBM / kWM) + 32 * ti + 8 * (e / 4) + 4 * half + (e % 4);
+        if (full || (row < row_end && col < col_end))
+          out[static_cast<std::size_t>(row) * ldo + col] = acc[ti][tj][e];
       }
     }
   }
+}
+
+// C tiles of a split tail: the sum, in split order, of each tail tile's
+// `splits` partial tiles. One float4 of a tile row per thread.
+template <typename Cfg>
+__global__ __launch_bounds__(256) void sum_tail_kernel(float* __restrict__ C, int M, int N,
+                                                       TailSplit tail) {
+  constexpr int kBM = Cfg::kBM, kBN = Cfg::kBN;
+  const int tiles_m = (M + kBM - 1) / kBM;
+  const int tiles_n = (N + kBN - 1) / kBN;
+  const int t = blockIdx.y;  // tail tile
+  const int q = blockIdx.x * 256 + threadIdx.x;  // float4 of the tile
+  const int lr = q / (kBN / 4);
+  const int lc = 4 * (q % (kBN / 4));
+  int tm, tn;
+  grouped_tile(tail.full_tiles + t, tiles_m, tiles_n, &tm, &tn);
+  const int row = tm * kBM + lr;
+  const int col = tn * kBN + lc;
+  if (lr >= kBM || row >= M || col >= N) return;
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sp = 0; sp < tail.splits; ++sp) {
+    const f4 v = *reinterpret_cast<const f4*>(
+        tail.partial + static_cast<std::size_t>(sp * tail.tiles + t) * kBM * kBN +
+        static_cast<std::size_t>(lr) * kBN + lc);
+    sum += v;
+  }
+  float* const dst = C + static_cast<std::size_t>(row) * N + col;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (col + e < N) dst[e] = sum[e];
 }
 
 #undef OPL_LDS
@@ -1320,13 +1399,49 @@ hipError_t launch_gemm(const T* a, const T* b, float* c, int m, int n, int k,
 
 template <typename Cfg>
 hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
-                            int m, int n, int k, int ldb, hipStream_t stream) {
+                            int m, int n, int k, int ldb, hipStream_t stream,
+                            dma::TailSplit tail = {0, 0, 0, nullptr}) {
   const long long tiles = static_cast<long long>((m + Cfg::kBM - 1) / Cfg::kBM) *
                           ((n + Cfg::kBN - 1) / Cfg::kBN);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-  dma::gemm_f16_dma_kernel<Cfg><<<dim3(static_cast<unsigned>(tiles)), dim3(Cfg::kThreads),
-                                  0, stream>>>(a, b, c, m, n, k, ldb);
+  const long long blocks =
+      tail.splits > 0 ? tail.full_tiles + static_cast<long long>(tail.tiles) * tail.splits : tiles;
+  if constexpr (Cfg::kBM != 256) {  // split tails are for 256 x 256 tiles
+    if (tail.splits > 0) return hipErrorInvalidValue;
+  }
+  if (tail.splits > 0) {
+    dma::gemm_f16_dma_kernel<Cfg, Cfg::kBM == 256><<<dim3(static_cast<unsigned>(blocks)),
+                                          dim3(Cfg::kThreads), 0, stream>>>(a, b, c, m, n, k,
+                                                                             ldb, tail);
+    if constexpr (Cfg::kBM == 256)
+      dma::sum_tail_kernel<Cfg><<<dim3(Cfg::kBM * Cfg::kBN / 4 / 256, tail.tiles), dim3(256), 0,
+                                  stream>>>(c, m, n, tail);
+  } else {
+    dma::gemm_f16_dma_kernel<Cfg><<<dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads),
+                                    0, stream>>>(a, b, c, m, n, k, ldb, tail);
+  }
   return hipGetLastError();
+}
+
+// A 256 x 256-tile grid that fills R >= 1 rounds of one workgroup per CU
+// plus a last round at most half full leaves most CUs idle for a whole
+// tile's time: the last round's tiles are then split along K into enough
+// parts to fill the CUs (at most 16, at least 4 K steps each) and summed
+// by a second launch. Measured on MI355X (us, unsplit vs split): 4096 x
+// 4160 x 4096 (272 tiles, 16 in the last round: 16 parts of 4 K steps)
+// 180-185 vs 138-143; 4160 x 4096 x 4032 (15 uneven parts) 184 vs 145;
+// 4100 x 4104 x 2048 (289 tiles, 33 last: 7 parts) 101 vs 93. Last
+// rounds more than half full stay unsplit (4096 x 11008: 688 tiles, 176
+// last).
+constexpr int kTailMaxSplits = 16;
+constexpr int kTailMinSteps = 4;
+
+int device_cus() {
+  int device = 0, cus = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return 0;
+  return cus;
 }
 
 // Grids of fewer 256 x 256 tiles than this run on 128 x 128 tiles. Measured
@@ -1336,12 +1451,33 @@ hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
 constexpr long long kSmallGridTiles = 160;
 
 hipError_t launch_gemm_f16_dma(const _Float16* a, const _Float16* b, float* c,
-                               int m, int n, int k, int ldb, hipStream_t stream) {
+                               int m, int n, int k, int ldb, hipStream_t stream,
+                               bool may_split_tail) {
   const long long big_tiles =
       static_cast<long long>((m + dma::BigTile::kBM - 1) / dma::BigTile::kBM) *
       ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
   if (big_tiles < kSmallGridTiles)
     return launch_dma_tiles<dma::SmallTile>(a, b, c, m, n, k, ldb, stream);
+  const int cus = may_split_tail ? device_cus() : 0;
+  const long long last = cus > 0 ? big_tiles % cus : 0;
+  const int steps = k / dma::kBK;
+  if (cus > 0 && big_tiles > cus && last > 0 && last <= cus / 2) {
+    int splits = static_cast<int>(cus / last);
+    if (splits > kTailMaxSplits) splits = kTailMaxSplits;
+    if (splits > steps / kTailMinSteps) splits = steps / kTailMinSteps;
+    if (splits >= 2) {
+      opl::ScratchLease lease(stream);
+      if (lease.status() != hipSuccess) return lease.status();
+      opl::Scratch scratch;
+      const std::size_t bytes = static_cast<std::size_t>(last) * splits *
+                                dma::BigTile::kBM * dma::BigTile::kBN * sizeof(float);
+      const hipError_t status = lease.get(bytes, &scratch);
+      if (status != hipSuccess) return status;
+      const dma::TailSplit tail{static_cast<int>(big_tiles - last), static_cast<int>(last),
+                                splits, static_cast<float*>(scratch.data)};
+      return launch_dma_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, stream, tail);
+    }
+  }
   return launch_dma_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, stream);
 }
 
@@ -1370,16 +1506,17 @@ extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
   const bool dma_offsets_fit = k < (1 << 22) && n < (1 << 24);
   if (dma_offsets_fit && k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
       opl::aligned16(b))
-    return launch_gemm_f16_dma(ha, hb, c, m, n, k, n, stream);
+    return launch_gemm_f16_dma(ha, hb, c, m, n, k, n, stream, true);
   if (dma_offsets_fit && worth_padding(m, n, k)) {
     opl::ScratchLease lease(stream);
     PaddedOperands p;
     const hipError_t status =
         pad_operands<_Float16>(ha, hb, m, n, k, dma::kBK, 8, stream, lease, &p);
     if (status != hipSuccess) return status;
+    // (the lease above already holds this stream's scratch: no tail split)
     return launch_gemm_f16_dma(static_cast<const _Float16*>(p.a),
                                static_cast<const _Float16*>(p.b), c, m, n, p.k,
-                               p.ldb, stream);
+                               p.ldb, stream, false);
   }
   return launch_gemm<_Float16>(ha, hb, c, m, n, k, stream);
 }

@@ -7,6 +7,8 @@
 //     launch;
 //   * GEMMs whose operands miss the fast kernels' shape / alignment rules:
 //     zero-padded aligned operand copies;
+//   * fp16 GEMMs whose last round of 256x256 tiles fills at most half the
+//     CUs: split-K partial tiles of that round, summed by a second launch;
 //   * register-staged attention on small grids: per-split partial outputs,
 //     merged by a second launch.
 // The reference launchers need none of this (src/reduce.cu:54-69 combines

@@ -394,12 +394,15 @@ def test_gemm_small_grid_tiles(hip, mnk, dtype):
 
 
 @pytest.mark.parametrize("mnk", [(4000, 2600, 1088), (4096, 2560, 64), (1000, 1000, 64),
-                                 (520, 2056, 192), (8192, 4096, 192), (4096, 12288, 64)])
+                                 (520, 2056, 192), (8192, 4096, 192), (4096, 12288, 64),
+                                 (4096, 4160, 4096), (4160, 4096, 4032), (4100, 4104, 2048)])
 def test_gemm_f16_step_counts(hip, mnk):
     """fp16 matrix-core tiles over odd numbers of 64-deep K steps (the loop
     runs steps in pairs), a single step, and ragged last tile rows and
-    columns; both tile sizes (176 and 160 big tiles, then small grids), and
-    grids of whole 16 x 16 super-tiles (32 x 16 and 16 x 48 big tiles)."""
+    columns; both tile sizes (176 and 160 big tiles, then small grids),
+    grids of whole 16 x 16 super-tiles (32 x 16 and 16 x 48 big tiles), and
+    grids one round plus 16 or 33 tiles long, whose last round is split
+    along K (16 parts of 4 steps, 15 uneven parts of 63 steps, 7 parts)."""
     m, n, k = mnk
     a = oracle.to_f16_bits(oracle.uniform(680 + m, (m, k)))
     b = oracle.to_f16_bits(oracle.uniform(681 + n, (k, n)))
