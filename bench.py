@@ -136,7 +136,7 @@ def parse_args():
 PROFILE_OPS = {"copy", "stream_copy", "reduce", "softmax", "softmax_ragged", "softmax_f16",
                "softmax_f16_ragged", "rmsnorm", "rmsnorm_ragged", "rmsnorm_f16",
                "rmsnorm_f16_ragged", "transpose", "transpose_ragged", "gemm_skinny",
-               "gemm_f32", "gemm_f16", "attention_f16"}
+               "gemm_f32", "gemm_f16", "vendor_gemm_f16", "attention_f16"}
 # Every HBM-bound kernel, for one counter pass that covers them all.
 BANDWIDTH_OPS = ["copy", "stream_copy", "reduce", "softmax", "softmax_ragged", "softmax_f16",
                  "softmax_f16_ragged", "rmsnorm", "rmsnorm_ragged", "rmsnorm_f16",
@@ -195,6 +195,11 @@ def profile_launchers(torch, lib, ptr, op: str):
                 out.append(lambda fn=fn, a=a, b=b, c=c, m=m:
                            fn(ptr(a), ptr(b), ptr(c), m, 4096, 4096, stream))
         return out
+    if op == "vendor_gemm_f16":  # not operatorlib: hipBLASLt on the same 8192^3 operands
+        n = 8192
+        a = (torch.rand(n, n, device=dev, generator=gen) * 2 - 1).half()
+        b = (torch.rand(n, n, device=dev, generator=gen) * 2 - 1).half()
+        return [lambda: torch.mm(a, b, out_dtype=torch.float32)]
     if op in ("gemm_f32", "gemm_f16"):
         n = 4096 if op == "gemm_f32" else 8192
         a = torch.rand(n, n, device=dev, generator=gen) * 2 - 1

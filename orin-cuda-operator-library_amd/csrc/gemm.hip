@@ -1,5 +1,6 @@
 // Row-major GEMM C[M,N] = A[M,K] * B[K,N] on the CDNA4 matrix cores.
-//   gemm_f16: fp16 A/B, v_mfma_f32_32x32x16_f16, fp32 accumulate and output
+//   gemm_f16: fp16 A/B, v_mfma_f32_16x16x32_f16 (direct-to-LDS kernel) or
+//             v_mfma_f32_32x32x16_f16 (register-staged), fp32 accumulate and output
 //   gemm_f32: fp32 A/B, v_mfma_f32_32x32x2_f32,  fp32 accumulate and output
 //
 // Reference: operatorlib::gemm_f16 / gemm_f32 (src/gemm.cu:440-479). The
@@ -7,7 +8,7 @@
 // kernels on divisibility; here the dispatch is, in order:
 //   * M <= 16 (decode shapes): the skinny kernels (namespace skinny), an
 //     HBM stream over B with split K and an ordered split sum;
-//   * gemm_f16_dma_kernel (fp16, K % 64 == 0, N % 8 == 0, 16-byte aligned
+//   * gemm_f16_dma_kernel (fp16, K % 32 == 0, N % 8 == 0, 16-byte aligned
 //     operands): direct global->LDS loads, described before the kernel;
 //     256 x 256 tiles, or 128 x 128 when the grid would leave CUs idle;
 //   * large shapes that miss those rules (e.g. 4095^3): zero-padded copies
@@ -360,16 +361,20 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 }
 
 // ---------------------------------------------------------------------------
-// gemm_f16_dma_kernel — the fp16 fast path (K % 64 == 0, N % 8 == 0, 16-byte
+// gemm_f16_dma_kernel — the fp16 fast path (K % 32 == 0, N % 8 == 0, 16-byte
 // aligned A and B).
 //
 //   * 256 x 256 C tile per 512-thread workgroup: 8 wavefronts as 2 (M) x 4
-//     (N), each owning 128 x 64 = 4 x 2 MFMA 32x32x16 blocks (128 fp32
+//     (N), each owning 128 x 64 = 8 x 4 MFMA 16x16x32 blocks (128 fp32
 //     accumulators, so two wavefronts fit per SIMD and one's LDS waits are
 //     covered by the other's MFMAs);
 //   * grids of fewer than 160 such tiles (medium M or N) use 128 x 128
 //     tiles instead: 4 wavefronts of 64 x 64, four times the workgroups,
 //     about 2x faster where 256 x 256 tiles would leave most CUs idle;
+//   * v_mfma_f32_16x16x32_f16 rather than 32x32x16: the same LDS bytes per
+//     flop and bit-identical sums, but the GPU holds a higher clock under
+//     the power limit with it (MI355X, a loop of MFMAs alone: 1.99 against
+//     1.70 GHz; with the GEMM's LDS reads: 1.75 against 1.55 GHz);
 //   * A and B are copied global -> LDS by buffer loads with the lds
 //     modifier (each lane writes 16 bytes at LDS base + 16 * lane) from
 //     per-step scalar bases, so operands never pass through VGPRs and no
@@ -380,33 +385,39 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 //     addresses 4 elements of row r and lane i receives element i % 4 of
 //     the lanes 4r + i / 4, r = 0..3;
 //   * XOR swizzles of the 16-byte chunks make every read conflict-free:
-//     A rows (128 B) use chunk ^ ((m >> 1) & 7), B rows (512 B) chunk ^
-//     4 * (k & 3); the DMA lane -> chunk mapping applies the same swizzle,
-//     and it keeps 128-byte (A) / 512-byte (B) contiguous global segments;
-//   * two LDS stages in separate arrays (so the compiler can see that the
-//     DMA into one does not alias the reads of the other), the loop unrolled
-//     by two. Each 64-deep K step is four k16 substeps; every substep reads
-//     the next substep's fragments under its MFMAs, one LDS read (two for
-//     128 x 128 tiles) after each MFMA (sched_group_barrier). The step's
-//     barrier comes before its last substep: by then every wave has read
-//     its last fragments from the stage and the next stage has landed, so
-//     the last substep's MFMAs cover both the next step's first fragment
-//     reads and the DMA refill of the stage just finished (interleaved the
-//     same way: the copies issued in one burst measured about 2% slower);
+//     A rows of 128 B (64-deep stages) use chunk ^ ((m >> 1) & 7), rows of
+//     64 B (32-deep stages) chunk ^ ((m >> 2) & 3); B rows chunk ^ 4 * (k &
+//     3) ^ 2 * (bit 3 of k); the DMA lane -> chunk mapping applies the same
+//     swizzle, and it keeps contiguous global segments per row;
+//   * stages in separate LDS arrays (so the compiler can see that the DMA
+//     into one does not alias the reads of another). Every 32-deep substep
+//     reads the next substep's fragments under its MFMAs, one LDS read or
+//     DMA issue after an MFMA at a time (sched_group_barrier);
+//   * 256 x 256 tiles with K % 64 == 0: two 64-deep stages, each step two
+//     substeps, the barrier between them: by then every wave has read its
+//     last fragments from the stage and the next stage has landed, so the
+//     second substep's MFMAs cover both the next step's first fragment
+//     reads and the DMA refill of the stage just finished;
+//   * 128 x 128 tiles and K % 64 == 32: four 32-deep stages, one substep
+//     and one barrier per step, copies issued three steps ahead (partial
+//     vmcnt waits). Measured against the two-stage schedule (us): 2048^3
+//     22.8 vs 27.6, 1000^3 19.6 vs 23.2 (128 x 128 tiles); 256 x 256 tiles
+//     lose (4096^3 109.6 vs 104.2), as their per-step barrier costs more
+//     than the deeper prefetch saves;
 //   * copies of steps past the end read through an empty buffer range
 //     (zeros, no memory access), so every step runs the same code;
 //   * M / N edges: source rows / columns are clamped into the matrix (their
 //     results are never stored), stores are masked.
-// Measured on MI355X (median of 8-launch groups): 4096^3 114-117 us, 8192^3
-// 887-910 us (1.20-1.24 PFLOP/s); hipBLASLt with the same fp32 C: 112-116
-// and 827-859 us. The previous schedule (all fragment reads of a substep
-// in one batch, copies issued in a burst at the top of the step, barrier at
-// its end) ran 122 / 925 us, bit-identical output.
+// Measured on MI355X (median of 8-launch groups): 4096^3 104-109 us, 8192^3
+// 852-871 us (1.26-1.29 PFLOP/s); hipBLASLt with the same fp32 C: 112-116
+// and 827-859 us. With v_mfma_f32_32x32x16_f16 the same schedule ran
+// 111-119 / 890-910 us, bit-identical output.
 // ---------------------------------------------------------------------------
 
 namespace dma {
 
 typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // Split of a grid's last, partly filled round: launch indices below
 // full_tiles take whole tiles; the `tiles` tiles after them in the grouped
@@ -422,17 +433,22 @@ struct TailSplit {
 #define OPL_LDS __attribute__((address_space(3)))
 
 // C tile configurations. BM x BN per workgroup, WM x WN wavefronts of
-// (BM / WM) x (BN / WN); K steps of 64. A rows in LDS are 128 bytes, B rows
-// 2 * BN bytes (BN / 8 16-byte chunks).
-template <int BM, int BN, int WM, int WN>
+// (BM / WM) x (BN / WN); K steps of BK (32 or 64) in `Stages` LDS stages.
+// A rows in LDS are 2 * BK bytes, B rows 2 * BN bytes (BN / 8 16-byte
+// chunks).
+template <int BM, int BN, int WM, int WN, int BK, int Stages>
 struct Tile {
-  static constexpr int kBM = BM, kBN = BN, kBK = 64;
+  static constexpr int kBM = BM, kBN = BN, kBK = BK;
   static constexpr int kWM = WM, kWN = WN;
+  static constexpr int kStages = Stages;
+  static constexpr int kSubsteps = BK / 32;  // MFMA k32 substeps per step
   static constexpr int kThreads = 64 * WM * WN;
-  static constexpr int kFM = BM / WM / 32;
-  static constexpr int kFN = BN / WN / 32;
-  static constexpr int kABytes = BM * kBK * 2;
-  static constexpr int kBBytes = kBK * BN * 2;
+  static constexpr int kFM = BM / WM / 16;
+  static constexpr int kFN = BN / WN / 16;
+  static constexpr int kARowBytes = BK * 2;
+  static constexpr int kAChunks = BK / 8;
+  static constexpr int kABytes = BM * BK * 2;
+  static constexpr int kBBytes = BK * BN * 2;
   static constexpr int kBRowBytes = BN * 2;
   static constexpr int kBChunks = BN / 8;
   static constexpr int kStage = kABytes + kBBytes;
@@ -441,16 +457,23 @@ struct Tile {
   static_assert(kABytes == kBBytes && kCopies * 16 * kThreads == kABytes,
                 "both operand tiles split evenly into 16-byte copies");
   static_assert(64 % kBChunks == 0, "a wavefront copies whole B rows");
+  static_assert((BK == 64 && Stages == 2) || (BK == 32 && Stages == 4),
+                "two 64-deep or four 32-deep stages");
+  // XOR swizzle of A row m's 16-byte chunks: rows 16 apart share it.
+  __device__ static int swizzle_a(int m) {
+    return kAChunks == 8 ? (m >> 1) & 7 : (m >> 2) & 3;
+  }
 };
 // 256 x 256: 8 wavefronts of 128 x 64, for grids that fill the GPU.
-using BigTile = Tile<256, 256, 2, 4>;
+using BigTile = Tile<256, 256, 2, 4, 64, 2>;
+// The same for K % 64 == 32.
+using BigTileK32 = Tile<256, 256, 2, 4, 32, 4>;
 // 128 x 128: 4 wavefronts of 64 x 64, four times the workgroups for the
 // same C, for grids that would leave CUs idle with BigTile.
-using SmallTile = Tile<128, 128, 2, 2>;
-constexpr int kBK = 64;  // K step of every tile configuration
+using SmallTile = Tile<128, 128, 2, 2, 32, 4>;
+constexpr int kBK = 32;  // K granularity of every tile configuration
 
-__device__ __forceinline__ int swizzle_a(int m) { return (m >> 1) & 7; }
-__device__ __forceinline__ int swizzle_b(int k) { return 4 * (k & 3); }
+__device__ __forceinline__ int swizzle_b(int k) { return 4 * (k & 3) ^ 2 * ((k >> 3) & 1); }
 
 template <typename Cfg>
 struct Fragments {
@@ -469,11 +492,9 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   constexpr int kFM = Cfg::kFM, kFN = Cfg::kFN;
   constexpr int kABytes = Cfg::kABytes, kCopies = Cfg::kCopies;
   constexpr int kBChunks = Cfg::kBChunks;
-  constexpr int kReads = kFM + 2 * kFN;  // LDS read instructions per k16 substep
+  constexpr int kReads = kFM + 2 * kFN;  // LDS read instructions per k32 substep
   constexpr int kIssues = 2 * kCopies;   // DMA instructions per K step
   static_assert(kWM == 2, "A fragment offsets assume two wavefront rows");
-  __shared__ __attribute__((aligned(1024))) unsigned char stage0[Cfg::kStage];
-  __shared__ __attribute__((aligned(1024))) unsigned char stage1[Cfg::kStage];
 
   const int tiles_m = (M + kBM - 1) / kBM;
   const int tiles_n = (N + kBN - 1) / kBN;
@@ -510,8 +531,8 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / opl::kWaveSize);
   const int wm = wave / kWN;
   const int wn = wave % kWN;
-  const int half = lane / 32;
-  const int l32 = lane % 32;
+  const int group = lane / 16;
+  const int gl = lane % 16;
 
   // DMA sources: copy j of this thread fills LDS chunk slot
   // (wave * kCopies + j) * 64 + lane of each operand tile. They are byte
@@ -523,8 +544,8 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
 #pragma unroll
   for (int j = 0; j < kCopies; ++j) {
     const int slot = (wave * kCopies + j) * 64 + lane;
-    const int m = slot / 8;
-    const int chunk = (slot % 8) ^ swizzle_a(m);
+    const int m = slot / Cfg::kAChunks;
+    const int chunk = (slot % Cfg::kAChunks) ^ Cfg::swizzle_a(m);
     a_dma[j] = (min(m0 + m, M - 1) - m0) * K * 2 + 16 * chunk;
     const int kk = (wave * kCopies + j) * (64 / kBChunks) + lane / kBChunks;
     const int col = n0 + 8 * ((lane % kBChunks) ^ swizzle_b(kk));
@@ -558,129 +579,174 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
     }
   };
 
-  // Fragment byte offsets inside a stage. A: the swizzle (m >> 1) & 7 of
-  // row m = wm * BM / 2 + 32 ti + l32 does not depend on ti, so one VGPR
-  // per k16 substep s serves every ti (rows 32 apart are 4096 bytes
-  // apart). B: k & 3 = gl / 4 for every s and half-row r, so one VGPR per
-  // tj serves every s and r (16 rows further per s, 4 rows per r).
-  constexpr int kBSubstep = 16 * Cfg::kBRowBytes;
-  unsigned a_lane[4];
+  // Fragment byte offsets inside a stage (MFMA 16x16x32: lane l supplies
+  // row / column l % 16 and the 8-element k chunk l / 16 of a k32 substep).
+  // A: row m = wm * BM / 2 + 16 ti + l % 16 has the same swizzle for every
+  // ti (rows 16 apart), so one VGPR per substep s serves every ti. B: k & 3
+  // and bit 3 of k are the same for every s and both 4-row halves, so one
+  // VGPR per tj serves every s and half.
+  constexpr int kBSubstep = 32 * Cfg::kBRowBytes;
+  unsigned a_lane[Cfg::kSubsteps];
   {
-    const int m = wm * (kBM / kWM) + l32;
+    const int m = wm * (kBM / kWM) + gl;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      a_lane[s] = m * 128 + (((2 * s + half) ^ swizzle_a(m)) * 16);
+    for (int s = 0; s < Cfg::kSubsteps; ++s)
+      a_lane[s] = m * Cfg::kARowBytes + (((4 * s + group) ^ Cfg::swizzle_a(m)) * 16);
   }
-  const int group = lane / 16;
-  const int gl = lane % 16;
   unsigned b_lane[kFN];
 #pragma unroll
   for (int tj = 0; tj < kFN; ++tj) {
-    const int n = wn * (kBN / kWN) + 32 * tj + 16 * (group % 2) + 4 * (gl % 4);
-    const int k = 8 * (group / 2) + gl / 4;
+    const int n = wn * (kBN / kWN) + 16 * tj + 4 * (gl % 4);
+    const int k = 8 * group + gl / 4;
     b_lane[tj] = kABytes + k * Cfg::kBRowBytes + (((n / 8) ^ swizzle_b(k)) * 16) + (n % 8) * 2;
   }
 
-  floatx16 acc[kFM][kFN];
+  floatx4 acc[kFM][kFN];
 #pragma unroll
   for (int i = 0; i < kFM; ++i)
 #pragma unroll
     for (int j = 0; j < kFN; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+      for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
 
+  // Fragments of substep s, read in the order the MFMAs use them (ti-major):
+  // A 0, every B, then the other A.
+  auto load_a = [&](const unsigned char* st, int s, Fragments<Cfg>& f, int t) {
+    f.a[t] = *reinterpret_cast<const half8*>(st + a_lane[s] + t * 16 * Cfg::kARowBytes);
+  };
   auto load = [&](const unsigned char* st, int s, Fragments<Cfg>& f) {
+    load_a(st, s, f, 0);
 #pragma unroll
-    for (int t = 0; t < (kFM > kFN ? kFM : kFN); ++t) {
-      if (t < kFM) f.a[t] = *reinterpret_cast<const half8*>(st + a_lane[s] + t * 4096);
-      if (t < kFN) {
-        const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-            (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s));
-        const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-            (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s + kBSubstep / 4));
-        half8 b;
+    for (int t = 0; t < kFN; ++t) {
+      const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+          (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s));
+      const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+          (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s + 4 * Cfg::kBRowBytes));
+      half8 b;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          b[e] = lo[e];
-          b[4 + e] = hi[e];
-        }
-        f.b[t] = b;
+      for (int e = 0; e < 4; ++e) {
+        b[e] = lo[e];
+        b[4 + e] = hi[e];
       }
+      f.b[t] = b;
     }
+#pragma unroll
+    for (int t = 1; t < kFM; ++t) load_a(st, s, f, t);
   };
   auto mma = [&](const Fragments<Cfg>& f) {
 #pragma unroll
     for (int ti = 0; ti < kFM; ++ti)
 #pragma unroll
       for (int tj = 0; tj < kFN; ++tj)
-        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
             f.a[ti], f.b[tj], acc[ti][tj], 0, 0, 0);
   };
   // Scheduling groups for one substep: each MFMA followed by its share of
   // the LDS reads (the next substep's fragments) and, with_dma, of the DMA
-  // issues, so reads and copies issue in the MFMAs' shadow instead of in a
-  // burst (one of each per MFMA for 256 x 256 tiles, two for 128 x 128).
+  // issues, spread evenly, so reads and copies issue in the MFMAs' shadow
+  // instead of in a burst.
   constexpr int kMfmas = kFM * kFN;
-  constexpr int kReadsPer = (kReads + kMfmas - 1) / kMfmas;
-  constexpr int kIssuesPer = (kIssues + kMfmas - 1) / kMfmas;
+  static_assert(kMfmas >= kReads && kMfmas >= kIssues, "at most one read and copy per MFMA");
   auto interleave = [&](bool with_dma) {
 #pragma unroll
     for (int i = 0; i < kMfmas; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      if (i * kReadsPer < kReads)
-        __builtin_amdgcn_sched_group_barrier(0x100, kReadsPer, 0);  // DS read
-      if (with_dma && i * kIssuesPer < kIssues)
-        __builtin_amdgcn_sched_group_barrier(0x010, kIssuesPer, 0);  // VMEM
+      if ((i + 1) * kReads / kMfmas != i * kReads / kMfmas)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (with_dma && (i + 1) * kIssues / kMfmas != i * kIssues / kMfmas)
+        __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // VMEM
     }
   };
-  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(0): this wave's LDS reads and
-  // DMA copies complete. The release fence of __syncthreads() does not
-  // wait for the copies, so the wait is explicit and the barrier bare.
-  auto sync_stage = [] {
-    __builtin_amdgcn_s_waitcnt(0x0070);
+  // s_waitcnt vmcnt(n) expcnt(7) lgkmcnt(0): this wave's LDS reads and all
+  // but its newest n DMA copies are complete. The release fence of
+  // __syncthreads() does not wait for the copies, so the wait is explicit
+  // and the barrier bare.
+  auto wait_copies = [](auto outstanding) {
+    constexpr int n = decltype(outstanding)::value;
+    static_assert(n < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x70);
+  };
+  // Every wave's copies of all but the newest kStages - 2 steps have landed
+  // and no wave still reads the stage to be refilled.
+  auto sync_stage = [&] {
+    wait_copies(std::integral_constant<int, (Cfg::kStages - 2) * kIssues>());
     asm volatile("s_barrier" ::: "memory");
   };
 
-  // Step `step` computes from `cur` (complete); `nxt` holds step + 1 (in
-  // flight). Substeps 0-2 each read the next substep's fragments from
-  // `cur` under their MFMAs. Then every wave has finished reading `cur`
-  // and step + 1 has landed (sync_stage), so substep 3 refills `cur` with
-  // step + 2 and reads the next step's first fragments from `nxt` under
-  // its MFMAs: the barrier never waits on an LDS read.
   Fragments<Cfg> f0, f1;
-  auto tile = [&](unsigned char* cur, unsigned char* nxt, int step) {
-    load(cur, 1, f1);
-    mma(f0);
-    interleave(false);
+  if constexpr (Cfg::kStages == 2) {
+    __shared__ __attribute__((aligned(1024))) unsigned char stage0[Cfg::kStage];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage1[Cfg::kStage];
+    // Step `step` computes from `cur` (complete); `nxt` holds step + 1 (in
+    // flight). Substep 0 reads substep 1's fragments from `cur` under its
+    // MFMAs. Then every wave has finished reading `cur` and step + 1 has
+    // landed (sync_stage), so substep 1 refills `cur` with step + 2 and
+    // reads the next step's first fragments from `nxt` under its MFMAs: the
+    // barrier never waits on an LDS read.
+    auto tile = [&](unsigned char* cur, unsigned char* nxt, int step) {
+      load(cur, 1, f1);
+      mma(f0);
+      interleave(false);
+      __builtin_amdgcn_sched_barrier(0);
+      sync_stage();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(cur, step + 2);
+      load(nxt, 0, f0);
+      mma(f1);
+      interleave(true);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    issue(stage0, 0);
+    issue(stage1, 1);
+    wait_copies(std::integral_constant<int, kIssues>());
+    asm volatile("s_barrier" ::: "memory");
+    load(stage0, 0, f0);
     __builtin_amdgcn_sched_barrier(0);
-    load(cur, 2, f0);
-    mma(f1);
-    interleave(false);
+    int step = 0;
+    for (; step + 1 < steps; step += 2) {
+      tile(stage0, stage1, step);
+      tile(stage1, stage0, step + 1);
+    }
+    if (step < steps) tile(stage0, stage1, step);
+  } else {
+    __shared__ __attribute__((aligned(1024))) unsigned char stage0[Cfg::kStage];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage1[Cfg::kStage];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage2[Cfg::kStage];
+    __shared__ __attribute__((aligned(1024))) unsigned char stage3[Cfg::kStage];
+    // Step `step` computes from fragments already in registers (`cur`, read
+    // from stage step % 4 during the previous step). At its top every wave
+    // has finished reading stage step % 4 and step + 1 has landed
+    // (sync_stage), so the step refills stage step % 4 with step + 4 and
+    // reads step + 1's fragments from `next` under its MFMAs.
+    auto tile = [&](unsigned char* refill, const unsigned char* next, int step,
+                    const Fragments<Cfg>& cur, Fragments<Cfg>& nxt) {
+      sync_stage();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(refill, step + 4);
+      load(next, 0, nxt);
+      mma(cur);
+      interleave(true);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    issue(stage0, 0);
+    issue(stage1, 1);
+    issue(stage2, 2);
+    issue(stage3, 3);
+    wait_copies(std::integral_constant<int, 3 * kIssues>());
+    asm volatile("s_barrier" ::: "memory");
+    load(stage0, 0, f0);
     __builtin_amdgcn_sched_barrier(0);
-    load(cur, 3, f1);
-    mma(f0);
-    interleave(false);
-    __builtin_amdgcn_sched_barrier(0);
-    sync_stage();
-    __builtin_amdgcn_sched_barrier(0);
-    issue(cur, step + 2);
-    load(nxt, 0, f0);
-    mma(f1);
-    interleave(true);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  issue(stage0, 0);
-  issue(stage1, 1);
-  sync_stage();
-  load(stage0, 0, f0);
-  __builtin_amdgcn_sched_barrier(0);
-  int step = 0;
-  for (; step + 1 < steps; step += 2) {
-    tile(stage0, stage1, step);
-    tile(stage1, stage0, step + 1);
+    int step = 0;
+    for (; step + 4 <= steps; step += 4) {
+      tile(stage0, stage1, step, f0, f1);
+      tile(stage1, stage2, step + 1, f1, f0);
+      tile(stage2, stage3, step + 2, f0, f1);
+      tile(stage3, stage0, step + 3, f1, f0);
+    }
+    if (step < steps) tile(stage0, stage1, step, f0, f1);
+    if (step + 1 < steps) tile(stage1, stage2, step + 1, f1, f0);
+    if (step + 2 < steps) tile(stage2, stage3, step + 2, f0, f1);
   }
-  if (step < steps) tile(stage0, stage1, step);
   __builtin_amdgcn_s_waitcnt(0);  // the last (empty) copies
 
   // A tail part writes its whole tile, row-major, to its partial slot;
@@ -696,10 +762,10 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   for (int ti = 0; ti < kFM; ++ti) {
 #pragma unroll
     for (int tj = 0; tj < kFN; ++tj) {
-      const int col = wn * (kBN / kWN) + 32 * tj + l32;
+      const int col = wn * (kBN / kWN) + 16 * tj + gl;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = wm * (kBM / kWM) + 32 * ti + 8 * (e / 4) + 4 * half + (e % 4);
+      for (int e = 0; e < 4; ++e) {
+        const int row = wm * (kBM / kWM) + 16 * ti + 4 * group + e;
         if (full || (row < row_end && col < col_end))
           out[static_cast<std::size_t>(row) * ldo + col] = acc[ti][tj][e];
       }
@@ -1426,7 +1492,7 @@ hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
 // A 256 x 256-tile grid that fills R >= 1 rounds of one workgroup per CU
 // plus a last round at most half full leaves most CUs idle for a whole
 // tile's time: the last round's tiles are then split along K into enough
-// parts to fill the CUs (at most 16, at least 4 K steps each) and summed
+// parts to fill the CUs (at most 16, at least 256 deep each) and summed
 // by a second launch. Measured on MI355X (us, unsplit vs split): 4096 x
 // 4160 x 4096 (272 tiles, 16 in the last round: 16 parts of 4 K steps)
 // 180-185 vs 138-143; 4160 x 4096 x 4032 (15 uneven parts) 184 vs 145;
@@ -1434,7 +1500,7 @@ hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
 // rounds more than half full stay unsplit (4096 x 11008: 688 tiles, 176
 // last).
 constexpr int kTailMaxSplits = 16;
-constexpr int kTailMinSteps = 4;
+constexpr int kTailMinDepth = 256;
 
 int device_cus() {
   int device = 0, cus = 0;
@@ -1450,35 +1516,51 @@ int device_cus() {
 // 4096 (180) 102.8 vs 110.0; 4096^3 (256) 121.1 vs 136.5.
 constexpr long long kSmallGridTiles = 160;
 
+// 256 x 256 tiles (Big: BigTile or BigTileK32), the last round split
+// along K when it is at most half full.
+template <typename Big>
+hipError_t launch_big_tiles(const _Float16* a, const _Float16* b, float* c, int m, int n,
+                            int k, int ldb, long long big_tiles, hipStream_t stream,
+                            bool may_split_tail) {
+  const int cus = may_split_tail ? device_cus() : 0;
+  const long long last = cus > 0 ? big_tiles % cus : 0;
+  if (cus > 0 && big_tiles > cus && last > 0 && last <= cus / 2) {
+    int splits = static_cast<int>(cus / last);
+    if (splits > kTailMaxSplits) splits = kTailMaxSplits;
+    if (splits > k / kTailMinDepth) splits = k / kTailMinDepth;
+    if (splits >= 2) {
+      opl::ScratchLease lease(stream);
+      if (lease.status() != hipSuccess) return lease.status();
+      opl::Scratch scratch;
+      const std::size_t bytes =
+          static_cast<std::size_t>(last) * splits * Big::kBM * Big::kBN * sizeof(float);
+      const hipError_t status = lease.get(bytes, &scratch);
+      if (status != hipSuccess) return status;
+      const dma::TailSplit tail{static_cast<int>(big_tiles - last), static_cast<int>(last),
+                                splits, static_cast<float*>(scratch.data)};
+      return launch_dma_tiles<Big>(a, b, c, m, n, k, ldb, stream, tail);
+    }
+  }
+  return launch_dma_tiles<Big>(a, b, c, m, n, k, ldb, stream);
+}
+
+// k % dma::kBK == 0.
 hipError_t launch_gemm_f16_dma(const _Float16* a, const _Float16* b, float* c,
                                int m, int n, int k, int ldb, hipStream_t stream,
                                bool may_split_tail) {
+  static_assert(dma::BigTile::kBM == dma::BigTileK32::kBM &&
+                    dma::BigTile::kBN == dma::BigTileK32::kBN,
+                "one big tile size");
   const long long big_tiles =
       static_cast<long long>((m + dma::BigTile::kBM - 1) / dma::BigTile::kBM) *
       ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
   if (big_tiles < kSmallGridTiles)
     return launch_dma_tiles<dma::SmallTile>(a, b, c, m, n, k, ldb, stream);
-  const int cus = may_split_tail ? device_cus() : 0;
-  const long long last = cus > 0 ? big_tiles % cus : 0;
-  const int steps = k / dma::kBK;
-  if (cus > 0 && big_tiles > cus && last > 0 && last <= cus / 2) {
-    int splits = static_cast<int>(cus / last);
-    if (splits > kTailMaxSplits) splits = kTailMaxSplits;
-    if (splits > steps / kTailMinSteps) splits = steps / kTailMinSteps;
-    if (splits >= 2) {
-      opl::ScratchLease lease(stream);
-      if (lease.status() != hipSuccess) return lease.status();
-      opl::Scratch scratch;
-      const std::size_t bytes = static_cast<std::size_t>(last) * splits *
-                                dma::BigTile::kBM * dma::BigTile::kBN * sizeof(float);
-      const hipError_t status = lease.get(bytes, &scratch);
-      if (status != hipSuccess) return status;
-      const dma::TailSplit tail{static_cast<int>(big_tiles - last), static_cast<int>(last),
-                                splits, static_cast<float*>(scratch.data)};
-      return launch_dma_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, stream, tail);
-    }
-  }
-  return launch_dma_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, stream);
+  if (k % dma::BigTile::kBK == 0)
+    return launch_big_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, big_tiles, stream,
+                                          may_split_tail);
+  return launch_big_tiles<dma::BigTileK32>(a, b, c, m, n, k, ldb, big_tiles, stream,
+                                           may_split_tail);
 }
 
 }  // namespace

@@ -247,7 +247,7 @@ def test_rmsnorm_pins(hip):
 # -------------------------------------------------------------------------- gemm
 
 # The reference smoke matrix (tests/gemm_smoke.cu:141-148) plus shapes that
-# exercise this library's fp16 global->LDS path at its M / N edges (K % 64 == 0,
+# exercise this library's fp16 global->LDS path at its M / N edges (K % 32 == 0,
 # N % 8 == 0, partial 256-wide tiles) and its fallback paths.
 GEMM_SMALL = [(1, 256, 64), (16, 128, 64), (128, 64, 32), (37, 65, 71), (7, 37, 23),
               (128, 128, 32), (16, 128, 32), (32, 32, 32), (17, 19, 23),
@@ -395,14 +395,20 @@ def test_gemm_small_grid_tiles(hip, mnk, dtype):
 
 @pytest.mark.parametrize("mnk", [(4000, 2600, 1088), (4096, 2560, 64), (1000, 1000, 64),
                                  (520, 2056, 192), (8192, 4096, 192), (4096, 12288, 64),
-                                 (4096, 4160, 4096), (4160, 4096, 4032), (4100, 4104, 2048)])
+                                 (4096, 4160, 4096), (4160, 4096, 4032), (4100, 4104, 2048),
+                                 (1000, 1000, 32), (600, 1100, 96), (1000, 700, 224),
+                                 (520, 2056, 160), (4096, 2560, 96), (4000, 2600, 1056),
+                                 (4096, 4096, 4128), (4096, 4160, 4128)])
 def test_gemm_f16_step_counts(hip, mnk):
-    """fp16 matrix-core tiles over odd numbers of 64-deep K steps (the loop
-    runs steps in pairs), a single step, and ragged last tile rows and
-    columns; both tile sizes (176 and 160 big tiles, then small grids),
-    grids of whole 16 x 16 super-tiles (32 x 16 and 16 x 48 big tiles), and
-    grids one round plus 16 or 33 tiles long, whose last round is split
-    along K (16 parts of 4 steps, 15 uneven parts of 63 steps, 7 parts)."""
+    """fp16 matrix-core tiles over every step-count remainder of their
+    loops: 256 x 256 tiles with K % 64 == 0 run 64-deep steps in pairs (odd
+    counts, a single step); 128 x 128 tiles (small grids) and 256 x 256
+    tiles with K % 64 == 32 run 32-deep steps in fours (1, 2, 3, 5, 6, 7,
+    33 and 129 steps); ragged last tile rows and columns; grids of whole
+    16 x 16 super-tiles (32 x 16 and 16 x 48 big tiles); and grids one round
+    plus 16 or 33 tiles long, whose last round is split along K (16 parts of
+    4 steps, 15 uneven parts of 63 steps, 7 parts, and 16 uneven parts of
+    32-deep steps)."""
     m, n, k = mnk
     a = oracle.to_f16_bits(oracle.uniform(680 + m, (m, k)))
     b = oracle.to_f16_bits(oracle.uniform(681 + n, (k, n)))
