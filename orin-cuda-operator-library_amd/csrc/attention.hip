@@ -1,6 +1,7 @@
 // FlashAttention-style forward on the CDNA4 matrix cores.
-//   attention_f16: fp16 Q/K/V, v_mfma_f32_32x32x16_f16, fp32 scores and
-//                  online-softmax state, P rounded to fp16 for P.V, fp32 out
+//   attention_f16: fp16 Q/K/V, v_mfma_f32_16x16x32_f16 (fast path) or
+//                  32x32x16, fp32 scores and online-softmax state, P rounded
+//                  to fp16 for P.V, fp32 out
 //   attention_f32: fp32 Q/K/V, v_mfma_f32_32x32x2_f32, all fp32
 //
 // Reference: operatorlib::attention_f16 / attention_f32
@@ -9,8 +10,10 @@
 // computed with the online recurrence m' = max(m, x), a = e^(m - m'),
 // l' = a l + sum e^(x - m'), O' = a O + e^(x - m') V (src/attention.cu:116-134,
 // :296-349) so no S x S matrix is ever stored. As in the reference FP16
-// path, P is rounded to fp16 before the P.V product and the row sum uses the
-// unrounded fp32 values (src/attention.cu:313-320).
+// path, P is rounded to fp16 before the P.V product; the reference's row
+// sum adds the unrounded fp32 values (src/attention.cu:313-320), as does
+// attention_mfma_kernel, while the fp16 fast path adds the rounded ones on
+// the matrix cores (a relative difference of at most 2^-11 per term).
 //
 // Two kernels share the design below: attention_f16_dma_kernel (fp16,
 // head_dim 64/128, S % 128 == 0, aligned tensors; described before it) and
@@ -553,9 +556,14 @@ hipError_t launch_attention(const T* q, const T* k, const T* v, float* out, int 
 
 // ---------------------------------------------------------------------------
 // attention_f16_dma_kernel — fp16 fast path (head_dim 64 or 128, S % 128 == 0,
-// 16-byte aligned tensors). Same maths and lane layout as
-// attention_mfma_kernel; its running max moves lazily (below), so results
-// agree up to rounding. What changes is how K and V reach the matrix cores:
+// 16-byte aligned tensors). Same maths as attention_mfma_kernel; its running
+// max moves lazily (below) and its row sums add the fp16-rounded p that P.V
+// uses, so results agree up to rounding. What changes:
+//   * v_mfma_f32_16x16x32_f16 instead of 32x32x16: the same flops per LDS
+//     byte, but the GPU holds a higher clock under the power limit with it.
+//     A wavefront's 32 query rows are two 16-row blocks (qc); S^T = K Q^T
+//     comes in 16 x 16 blocks, so lane l holds query 16 qc + l % 16 and keys
+//     4 (l / 16) + e of each 16-key block; a row's keys span four lanes;
 //   * K / V tiles are copied global -> LDS by buffer loads with the lds
 //     modifier (buffer_load_dwordx4 ... lds: no VGPR staging, no ds_write,
 //     no register transpose of V); the tile's position is a scalar offset;
@@ -565,19 +573,23 @@ hipError_t launch_attention(const T* q, const T* k, const T* v, float* out, int 
 //     realises the key order of the P^T accumulator registers;
 //   * XOR-swizzled 16-byte chunks keep every LDS read conflict-free: K rows
 //     use chunk ^ (row & 15) (D = 128) or ^ ((row >> 1) & 7) (D = 64), V rows
-//     chunk ^ 4 * (row & 3) / ^ 4 * ((row >> 1) & 1); the swizzle terms are
-//     lane constants, so per-tile offsets fold into instruction immediates;
-//   * ~200 VGPRs and 64 KiB of LDS, so two 4-wavefront workgroups share a CU
+//     chunk ^ (4 (row & 3) ^ 2 ((row >> 2) & 1)) / ^ 2 ((row >> 1) & 3); the
+//     swizzle terms are lane constants, so per-tile offsets fold into
+//     instruction immediates;
+//   * row sums on the matrix cores (ones x P^T), one rescale decision per
+//     64-key tile;
+//   * ~250 VGPRs and 64 KiB of LDS, so two 4-wavefront workgroups share a CU
 //     (the LDS is the limit): one wavefront's softmax VALU work overlaps
 //     the other's MFMAs.
-// Measured on MI355X, B4 H32 S8192 D128 causal: 2.21-2.42 ms (910-994 TFLOP/s
-// effective; the lower figure under sustained load), vs 472 TFLOP/s for
-// PyTorch's SDPA on the same box.
+// Measured on MI355X, B4 H32 S8192 D128 causal: 2.07 ms (1060 TFLOP/s
+// effective; 2.23 ms with 32x32x16 MFMAs and VALU row sums), vs 474 TFLOP/s
+// for PyTorch's SDPA on the same box.
 // ---------------------------------------------------------------------------
 
 namespace dma {
 
 typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 #define OPL_LDS __attribute__((address_space(3)))
 
 constexpr int kXcds = 8;
@@ -624,14 +636,27 @@ struct Layout {
   static constexpr int kChunks = kRowBytes / 16;
   static constexpr int kTile = kTileKeys * kRowBytes;  // one K or V tile
   static constexpr int kStage = 2 * kTile;
-  static constexpr int kSteps = D / 16;  // QK^T k-steps
-  static constexpr int kDTiles = D / 32;
+  static constexpr int kSteps = D / 32;    // QK^T k32 steps
+  static constexpr int kDBlocks = D / 16;  // 16-dim blocks of O^T
+  // K rows: 16 consecutive rows read one logical chunk (one 16-lane group)
+  // and land on 16 different physical chunks.
   __device__ static int swizzle_k(int row) {
     return D == 128 ? (row & 15) : ((row >> 1) & 7);
   }
+  // V rows: a ds_read_b64_tr_b16 group reads 8 bytes from each of 4 rows
+  // (4 lanes per row); the 4 rows, and the next group's 4, land on
+  // different banks.
   __device__ static int swizzle_v(int row) {
-    return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1);
+    return D == 128 ? ((4 * (row & 3)) ^ (2 * ((row >> 2) & 1)))
+                    : 2 * ((row >> 1) & 3);
   }
+};
+
+// Scores of one 32-key half for a wavefront's 32 query rows: [kb][qc] is
+// the 16 x 16 block of keys 16 kb.. and queries 16 qc.. (S^T layout: lane l
+// holds query l % 16, keys 4 (l / 16) + e).
+struct HalfScores {
+  floatx4 v[2][2];
 };
 
 // kGroups > 1 (small grids): kGroups groups of kW wavefronts share the
@@ -694,20 +719,26 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
                                            threadIdx.x / opl::kWaveSize / kW);
   unsigned char* const st0 = stage0 + group * L::kStage;
   unsigned char* const st1 = stage1 + group * L::kStage;
-  const int half = lane / 32;
-  const int l32 = lane % 32;
+  // v_mfma_f32_16x16x32_f16 lane roles: lane l supplies row / column
+  // l % 16 of its operands and their 8-element k chunk l / 16; its
+  // accumulator holds column l % 16, rows 4 (l / 16) + e, e = 0..3.
+  const int col = lane % 16;
+  const int quad = lane / 16;
   const int wave_row0 = q0 + wave * kRowsPerWave;
-  const int my_row = wave_row0 + l32;
   const std::size_t head = static_cast<std::size_t>(bh) * S * D;
   const _Float16* qh = Q + head;
   const _Float16* kh = K + head;
   const _Float16* vh = V + head;
 
-  half8 qf[L::kSteps];
+  // Q^T operand of query block qc: query wave_row0 + 16 qc + col, dims
+  // 32 c + 8 quad .. + 7.
+  half8 qf[2][L::kSteps];
 #pragma unroll
-  for (int c = 0; c < L::kSteps; ++c)
-    qf[c] = *reinterpret_cast<const half8*>(
-        qh + static_cast<std::size_t>(my_row) * D + 16 * c + 8 * half);
+  for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+    for (int c = 0; c < L::kSteps; ++c)
+      qf[qc][c] = *reinterpret_cast<const half8*>(
+          qh + static_cast<std::size_t>(wave_row0 + 16 * qc + col) * D + 32 * c + 8 * quad);
 
   // DMA: element offset of the chunk this lane copies, per copy.
   int k_src[kCopies], v_src[kCopies];
@@ -745,34 +776,52 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
       opl::buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave_s * kCopies + j) * 1024,
                         v_src[j], tile_bytes);
   };
-  // K^T-operand rows are l32 (+32 for the second 32-key block, an immediate).
+  // K operand: key row col of each 16-key block, chunk 4 c + quad. Rows 16
+  // apart share the swizzle, so the block and half offsets are immediates.
   int k_off[L::kSteps];
 #pragma unroll
   for (int c = 0; c < L::kSteps; ++c)
-    k_off[c] = l32 * L::kRowBytes + (((2 * c + half) ^ L::swizzle_k(l32)) * 16);
-  // V^T operand: key row 32kb + 16u + 8r + 4(g >> 1) + (gi >> 2), dim
-  // 32dt + 16(g & 1) + 4(gi & 3); only dt changes the swizzled address.
-  const int g = lane / 16;
-  const int gi = lane % 16;
-  int v_base[L::kDTiles];
+    k_off[c] = col * L::kRowBytes + (((4 * c + quad) ^ L::swizzle_k(col)) * 16);
+  // V^T operand of dim block db: lane l addresses 4 dims (16 db + 4 (col %
+  // 4) ..) of key row 4 quad + col / 4 and receives dim 16 db + col of key
+  // rows 4 quad + 0..3 (k slots 8 quad + 0..3); the read 16 rows on gives
+  // slots 8 quad + 4..7. That is the key order of the P^T registers below.
+  int v_base[L::kDBlocks];
 #pragma unroll
-  for (int dt = 0; dt < L::kDTiles; ++dt) {
-    const int row = 4 * (g >> 1) + (gi >> 2);
-    const int d = 32 * dt + 16 * (g & 1) + 4 * (gi & 3);
-    v_base[dt] = L::kTile + row * L::kRowBytes +
+  for (int db = 0; db < L::kDBlocks; ++db) {
+    const int row = 4 * quad + col / 4;
+    const int d = 16 * db + 4 * (col % 4);
+    v_base[db] = L::kTile + row * L::kRowBytes +
                  (((d >> 3) ^ L::swizzle_v(row)) * 16) + (d & 7) * 2;
   }
 
-  floatx16 o[L::kDTiles];
+  // O^T of query block qc, dim block db: lane l holds query 16 qc + col,
+  // dims 16 db + 4 quad + e.
+  floatx4 o[2][L::kDBlocks];
 #pragma unroll
-  for (int dt = 0; dt < L::kDTiles; ++dt)
+  for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
-  float row_max = -FLT_MAX;
-  float row_sum = 0.0f;
+    for (int db = 0; db < L::kDBlocks; ++db)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[qc][db][e] = 0.0f;
+  // Online-softmax state of the lane's two query rows.
+  float row_max[2] = {-FLT_MAX, -FLT_MAX};
   // Raw score above which the running max must move; -inf until the first
   // visible score.
-  float move_above = -INFINITY;
+  float move_above[2] = {-INFINITY, -INFINITY};
+  // Row sums on the matrix cores: an all-ones A operand times P^T gives
+  // every accumulator row the column sums of P^T, i.e. each lane the full
+  // sum of its query row's p (as rounded to fp16 for P.V) in all four
+  // elements. That replaces 32 VALU adds per tile and a wavefront with 4
+  // MFMAs (the vector ALUs, not the matrix cores, are the busier pipe).
+  floatx4 sums[2];
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sums[qc][e] = 0.0f;
+  half8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = static_cast<_Float16>(1.0f);
   const float inv_scale = 1.0f / score_scale_log2;
   const int visible_end = causal ? min(S, q0 + kRows) : S;
   const int tiles = (visible_end + kTileKeys - 1) / kTileKeys;
@@ -796,38 +845,56 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
       // product of half 0 (matrix cores) and the exponentials of both
       // halves (vector ALUs), and the scheduler can interleave them. A
       // 32-key tile is one such half.
-      auto scores = [&](int kb) {
-        floatx16 s;
+      auto scores = [&](int j) {
+        HalfScores s;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s[e] = 0.0f;
-        half8 a[L::kSteps];
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int c = 0; c < L::kSteps; ++c)
-          a[c] = *reinterpret_cast<const half8*>(
-              cur + k_off[c] + kb * 32 * L::kRowBytes);
-        // All K reads of the half are issued before the MFMA chain: with
-        // one workgroup per CU (small grids) nothing else hides their
-        // latency (B1 H12 S1024: 22.8 -> 22.3 us).
+          for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s.v[kb][qc][e] = 0.0f;
+        half8 a[2][L::kSteps];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int c = 0; c < L::kSteps; ++c)
+            a[kb][c] = *reinterpret_cast<const half8*>(
+                cur + k_off[c] + (32 * j + 16 * kb) * L::kRowBytes);
+        // All K reads of the half are issued before the MFMAs: with one
+        // workgroup per CU (small grids) nothing else hides their latency.
         __builtin_amdgcn_sched_barrier(0);
+        // Four independent accumulators, so no MFMA waits on the previous.
 #pragma unroll
         for (int c = 0; c < L::kSteps; ++c)
-          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[c], s, 0, 0, 0);
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int qc = 0; qc < 2; ++qc)
+              s.v[kb][qc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  a[kb][c], qf[qc][c], s.v[kb][qc], 0, 0, 0);
         return s;
       };
-      auto mask = [&](floatx16& s, int kb) {
+      auto mask = [&](HalfScores& s, int j) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = key0 + 32 * kb + 8 * (e / 4) + 4 * half + (e % 4);
-          if (key > my_row) s[e] = -INFINITY;
-        }
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qc = 0; qc < 2; ++qc)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int key = key0 + 32 * j + 16 * kb + 4 * quad + e;
+              if (key > wave_row0 + 16 * qc + col) s.v[kb][qc][e] = -INFINITY;
+            }
       };
-      // Max of this lane's 16 raw scores of a half (v_maximum3_f32: 8
-      // instructions). The row's other 16 scores sit in lane l ^ 32; the
-      // two are combined only when the max has to move (move_max).
-      auto lane_max = [&](const floatx16& s) {
-        float m = s[0];
+      // Max of this lane's 8 raw scores of query block qc in a half. The
+      // row's other 24 sit in lanes l ^ 16, l ^ 32, l ^ 48; they are
+      // combined only when the max has to move (move_max).
+      auto lane_max = [&](const HalfScores& s, int qc) {
+        float m = s.v[0][qc][0];
 #pragma unroll
-        for (int e = 1; e < 16; ++e) m = __builtin_elementwise_maximum(m, s[e]);
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = kb == 0 ? 1 : 0; e < 4; ++e)
+            m = __builtin_elementwise_maximum(m, s.v[kb][qc][e]);
         return m;
       };
       // Lazy rescaling: the running max m (log2 units) only moves when a
@@ -836,75 +903,89 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
       // skipped on almost every half-tile. Softmax is shift-invariant: the
       // result is the same up to rounding. The test compares raw scores
       // with move_above = (m + kLazyLog2) / scale, updated when m moves.
-      auto needs_move = [&](float lane_raw) {
-        return __builtin_amdgcn_ballot_w64(lane_raw > move_above) != 0;
+      auto needs_move = [&](float raw0, float raw1) {
+        return __builtin_amdgcn_ballot_w64(raw0 > move_above[0] ||
+                                           raw1 > move_above[1]) != 0;
       };
-      // Wave-uniform branch: every lane runs it, and both lanes of a row
-      // combine their halves, so they move to the same max.
-      auto move_max = [&](float lane_raw) {
-        const float raw = opl::max_lane_xor32(lane_raw);
-        const float new_max = fmaxf(row_max, raw * score_scale_log2);
-        const float alpha = opl::fast_exp2(row_max - new_max);
-        row_max = new_max;
-        move_above = (new_max + kLazyLog2) * inv_scale;
-        row_sum *= alpha;
+      // Wave-uniform branch: every lane runs it, and the four lanes of a
+      // row combine their maxima, so they move to the same max.
+      auto move_max = [&](float raw0, float raw1) {
+        const float lane_raw[2] = {raw0, raw1};
 #pragma unroll
-        for (int dt = 0; dt < L::kDTiles; ++dt)
+        for (int qc = 0; qc < 2; ++qc) {
+          const float raw = opl::max_lane_xor32(
+              opl::combine_xor16_f32<opl::MaxOp>(lane_raw[qc]));
+          const float new_max = fmaxf(row_max[qc], raw * score_scale_log2);
+          const float alpha = opl::fast_exp2(row_max[qc] - new_max);
+          row_max[qc] = new_max;
+          move_above[qc] = (new_max + kLazyLog2) * inv_scale;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-      };
-      auto exponentiate = [&](const floatx16& s, half8 (&pb)[2]) {
-        float psum = 0.0f;
+          for (int e = 0; e < 4; ++e) sums[qc][e] *= alpha;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = opl::fast_exp2(fmaf(s[e], score_scale_log2, -row_max));
-          psum += p;
-          pb[e / 8][e % 8] = static_cast<_Float16>(p);
+          for (int db = 0; db < L::kDBlocks; ++db)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[qc][db][e] *= alpha;
         }
-        return psum;
       };
-      auto accumulate = [&](int kb, const half8 (&pb)[2]) {
+      // P of query block qc as the B operand of P.V: k slots 8 quad + e are
+      // keys 4 quad + e of block 0, slots 8 quad + 4 + e those of block 1.
+      auto exponentiate = [&](const HalfScores& s, half8 (&pb)[2]) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int rows = (32 * kb + 16 * u) * L::kRowBytes;
+        for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
-          for (int dt = 0; dt < L::kDTiles; ++dt) {
-            const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                (OPL_LDS fp16x4*)(cur + v_base[dt] + rows));
-            const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                (OPL_LDS fp16x4*)(cur + v_base[dt] + rows + 8 * L::kRowBytes));
-            half8 a;
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              a[e] = lo[e];
-              a[4 + e] = hi[e];
-            }
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[u], o[dt], 0, 0, 0);
+            for (int e = 0; e < 4; ++e)
+              pb[qc][4 * kb + e] = static_cast<_Float16>(opl::fast_exp2(
+                  fmaf(s.v[kb][qc][e], score_scale_log2, -row_max[qc])));
+      };
+      auto accumulate = [&](int j, const half8 (&pb)[2]) {
+        const int rows = 32 * j * L::kRowBytes;
+#pragma unroll
+        for (int db = 0; db < L::kDBlocks; ++db) {
+          const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+              (OPL_LDS fp16x4*)(cur + v_base[db] + rows));
+          const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+              (OPL_LDS fp16x4*)(cur + v_base[db] + rows + 16 * L::kRowBytes));
+          half8 a;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            a[e] = lo[e];
+            a[4 + e] = hi[e];
           }
+#pragma unroll
+          for (int qc = 0; qc < 2; ++qc)
+            o[qc][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[qc], o[qc][db], 0, 0, 0);
         }
+#pragma unroll
+        for (int qc = 0; qc < 2; ++qc)
+          sums[qc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[qc], sums[qc], 0, 0, 0);
       };
+      // One rescale decision per tile, taken on both halves' maxima before
+      // either P.V: the O rescale then happens in O's own registers (a
+      // second decision after the first P.V made the compiler copy all 64
+      // accumulators on every tile that did not rescale). Measured on
+      // MI355X, B4 H32 S8192 causal: 2234 -> 2120 us; with the row sums on
+      // the matrix cores, 2075 us.
       auto body = [&](auto masked_tag) {
         constexpr bool kMasked = decltype(masked_tag)::value;
         half8 p0[2], p1[2];
-        floatx16 s0 = scores(0);
+        HalfScores s0 = scores(0);
         if constexpr (kMasked) mask(s0, 0);
-        const float c0 = lane_max(s0);
-        if (needs_move(c0)) move_max(c0);
-        if constexpr (kTileKeys == 32) {
-          row_sum += exponentiate(s0, p0);
-          accumulate(0, p0);
-        } else {
-          floatx16 s1 = scores(1);
-          row_sum += exponentiate(s0, p0);
-          accumulate(0, p0);
+        float a0 = lane_max(s0, 0);
+        float a1 = lane_max(s0, 1);
+        HalfScores s1;
+        if constexpr (kTileKeys == 64) {
+          s1 = scores(1);
           if constexpr (kMasked) mask(s1, 1);
-          const float c1 = lane_max(s1);
-          float ps1 = exponentiate(s1, p1);
-          if (needs_move(c1)) {
-            move_max(c1);  // after P.V of half 0, which used the old max
-            ps1 = exponentiate(s1, p1);
-          }
-          row_sum += ps1;
+          a0 = __builtin_elementwise_maximum(a0, lane_max(s1, 0));
+          a1 = __builtin_elementwise_maximum(a1, lane_max(s1, 1));
+        }
+        if (needs_move(a0, a1)) move_max(a0, a1);
+        exponentiate(s0, p0);
+        accumulate(0, p0);
+        if constexpr (kTileKeys == 64) {
+          exponentiate(s1, p1);
           accumulate(1, p1);
         }
       };
@@ -927,12 +1008,13 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     tile(st1, st0, i + 1);
   }
   if (i < iters) tile(st0, st1, i);
+  float row_sum[2] = {sums[0][0], sums[1][0]};
 
   // After the loop every stage is free (the last iteration ended with a
   // barrier and issued no copy). Exchange and staging blocks are wave
-  // contiguous: block (g, w) of 16 * kDTiles float4s per lane, lane
-  // contiguous, 64 * 16 * kDTiles bytes.
-  constexpr int kBlockBytes = L::kDTiles * 16 * opl::kWaveSize * 4;
+  // contiguous: block (g, w) of 2 * kDBlocks float4s per lane, lane
+  // contiguous, 64 * 32 * kDBlocks bytes.
+  constexpr int kBlockBytes = 2 * L::kDBlocks * 16 * opl::kWaveSize;
   static_assert(kArray % kBlockBytes == 0 && kW * kBlockBytes <= 2 * kArray,
                 "blocks tile the two stage arrays");
   auto block = [&](int index) -> float4* {
@@ -941,10 +1023,10 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   };
   if constexpr (kGroups > 1) {
     // Wavefront w of group g > 0 hands its state to wavefront w of group 0,
-    // which holds the same rows: O in block ((g - 1) * kW + w), max and sum
-    // at the end of stage1.
+    // which holds the same rows: O in block ((g - 1) * kW + w), the two
+    // rows' max and sum at the end of stage1.
     constexpr int kSlots = kW * opl::kWaveSize;
-    constexpr int kMLBytes = (kGroups - 1) * 2 * kSlots * 4;
+    constexpr int kMLBytes = (kGroups - 1) * 4 * kSlots * 4;
     static_assert((kGroups - 1) * kW * kBlockBytes <= 2 * kArray - kMLBytes,
                   "the exchange fits the stages");
     float* const xs = reinterpret_cast<float*>(stage1 + kArray - kMLBytes);
@@ -952,13 +1034,16 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     if (group > 0) {
       float4* const xo = block((group - 1) * kW + wave);
 #pragma unroll
-      for (int dt = 0; dt < L::kDTiles; ++dt)
+      for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          xo[(dt * 4 + q) * opl::kWaveSize + lane] =
-              make_float4(o[dt][4 * q], o[dt][4 * q + 1], o[dt][4 * q + 2], o[dt][4 * q + 3]);
-      xs[(group - 1) * 2 * kSlots + slot] = row_max;
-      xs[(group - 1) * 2 * kSlots + kSlots + slot] = row_sum;
+        for (int db = 0; db < L::kDBlocks; ++db)
+          xo[(qc * L::kDBlocks + db) * opl::kWaveSize + lane] =
+              make_float4(o[qc][db][0], o[qc][db][1], o[qc][db][2], o[qc][db][3]);
+#pragma unroll
+      for (int qc = 0; qc < 2; ++qc) {
+        xs[((group - 1) * 4 + qc) * kSlots + slot] = row_max[qc];
+        xs[((group - 1) * 4 + 2 + qc) * kSlots + slot] = row_sum[qc];
+      }
     }
     __syncthreads();
     if (group > 0) return;
@@ -967,48 +1052,52 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
 #pragma unroll
     for (int r = 1; r < kGroups; ++r) {
       const float4* const xo = block((r - 1) * kW + wave);
-      const float m1 = xs[(r - 1) * 2 * kSlots + slot];
-      const float l1 = xs[(r - 1) * 2 * kSlots + kSlots + slot];
-      const float m = fmaxf(row_max, m1);
-      const float a0 = opl::fast_exp2(row_max - m);
-      const float a1 = opl::fast_exp2(m1 - m);
-      row_max = m;
-      row_sum = row_sum * a0 + l1 * a1;
 #pragma unroll
-      for (int dt = 0; dt < L::kDTiles; ++dt)
+      for (int qc = 0; qc < 2; ++qc) {
+        const float m1 = xs[((r - 1) * 4 + qc) * kSlots + slot];
+        const float l1 = xs[((r - 1) * 4 + 2 + qc) * kSlots + slot];
+        const float m = fmaxf(row_max[qc], m1);
+        const float a0 = opl::fast_exp2(row_max[qc] - m);
+        const float a1 = opl::fast_exp2(m1 - m);
+        row_max[qc] = m;
+        row_sum[qc] = row_sum[qc] * a0 + l1 * a1;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 x = xo[(dt * 4 + q) * opl::kWaveSize + lane];
-          o[dt][4 * q] = o[dt][4 * q] * a0 + x.x * a1;
-          o[dt][4 * q + 1] = o[dt][4 * q + 1] * a0 + x.y * a1;
-          o[dt][4 * q + 2] = o[dt][4 * q + 2] * a0 + x.z * a1;
-          o[dt][4 * q + 3] = o[dt][4 * q + 3] * a0 + x.w * a1;
+        for (int db = 0; db < L::kDBlocks; ++db) {
+          const float4 x = xo[(qc * L::kDBlocks + db) * opl::kWaveSize + lane];
+          o[qc][db][0] = o[qc][db][0] * a0 + x.x * a1;
+          o[qc][db][1] = o[qc][db][1] * a0 + x.y * a1;
+          o[qc][db][2] = o[qc][db][2] * a0 + x.z * a1;
+          o[qc][db][3] = o[qc][db][3] * a0 + x.w * a1;
         }
+      }
     }
   }
 
   // O leaves through LDS so that every store instruction writes whole rows:
   // the accumulator gives a lane 4 consecutive dims of one row per float4
-  // (a store straight from it writes 32-byte pieces of 32 rows); re-read
+  // (a store straight from it writes 16-byte pieces of 16 rows); re-read
   // from the wave's own block, one float4 instruction covers 64 / (D / 4)
   // whole rows. The block is the one this wave alone read its merge input
   // from (or, with one group, a free one), so no other wave touches it.
   // Float4 c of row r sits at position c ^ (r % (D / 4)): both the writes
-  // (32 rows, one float4 position each) and the reads (one row per 32 or
-  // 16 lanes) spread over the banks. Measured on MI355X (us): B1 H12 S1024
-  // 17.2 -> 16.5, causal 16.7 -> 15.8; B4 H32 S8192 causal unchanged.
-  const float inv = 1.0f / opl::sum_lane_xor32(row_sum);
+  // (16 rows, one float4 position each) and the reads (one row per 32 or
+  // 16 lanes) spread over the banks.
+  float inv[2];
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc)
+    inv[qc] = 1.0f / row_sum[qc];
   {
     constexpr int kChunks4 = D / 4;  // float4s per output row
     float4* const stg = block(wave);
 #pragma unroll
-    for (int dt = 0; dt < L::kDTiles; ++dt)
+    for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
-      for (int gg = 0; gg < 4; ++gg) {
-        const int c = (32 * dt + 8 * gg + 4 * half) / 4;
-        stg[l32 * kChunks4 + (c ^ (l32 % kChunks4))] =
-            make_float4(o[dt][4 * gg] * inv, o[dt][4 * gg + 1] * inv,
-                        o[dt][4 * gg + 2] * inv, o[dt][4 * gg + 3] * inv);
+      for (int db = 0; db < L::kDBlocks; ++db) {
+        const int r = 16 * qc + col;
+        const int c = 4 * db + quad;
+        stg[r * kChunks4 + (c ^ (r % kChunks4))] =
+            make_float4(o[qc][db][0] * inv[qc], o[qc][db][1] * inv[qc],
+                        o[qc][db][2] * inv[qc], o[qc][db][3] * inv[qc]);
       }
     constexpr int kRowsPerStore = opl::kWaveSize / kChunks4;
     const int rr = lane / kChunks4;
