@@ -16,7 +16,7 @@
 // the matrix cores (a relative difference of at most 2^-11 per term).
 //
 // Two kernels share the design below: attention_f16_dma_kernel (fp16,
-// head_dim 64/128, S % 128 == 0, aligned tensors; described before it) and
+// head_dim 64/128, any S, aligned tensors; described before it) and
 // attention_mfma_kernel (every other shape and fp32), which stages K / V
 // through registers.
 //
@@ -555,7 +555,7 @@ hipError_t launch_attention(const T* q, const T* k, const T* v, float* out, int 
 }
 
 // ---------------------------------------------------------------------------
-// attention_f16_dma_kernel — fp16 fast path (head_dim 64 or 128, S % 128 == 0,
+// attention_f16_dma_kernel — fp16 fast path (head_dim 64 or 128, any S,
 // 16-byte aligned tensors). Same maths as attention_mfma_kernel; its running
 // max moves lazily (below) and its row sums add the fp16-rounded p that P.V
 // uses, so results agree up to rounding. What changes:
@@ -703,7 +703,10 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   // [x * per_xcd, (x + 1) * per_xcd), so the workgroups resident on one XCD
   // at a time belong to one or two heads and share that head's K/V tiles
   // in the XCD's L2 instead of streaming them from HBM per query block.
-  const int q_blocks = S / kRows;
+  // The last block of a head may run past S: its rows from S on load row
+  // S - 1 of Q and are not stored; keys from S on read zeros (the buffer
+  // range ends at the head) and are masked.
+  const int q_blocks = (S + kRows - 1) / kRows;
   const int total = q_blocks * BH;
   const int per_xcd = (total + kXcds - 1) / kXcds;
   const int w = static_cast<int>(blockIdx.x % kXcds) * per_xcd +
@@ -739,7 +742,8 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
 #pragma unroll
     for (int c = 0; c < L::kSteps; ++c)
       qf[qc][c] = *reinterpret_cast<const half8*>(
-          qh + static_cast<std::size_t>(wave_row0 + 16 * qc + col) * D + 32 * c + 8 * quad);
+          qh + static_cast<std::size_t>(min(wave_row0 + 16 * qc + col, S - 1)) * D +
+          32 * c + 8 * quad);
 
   // DMA: element offset of the chunk this lane copies, per copy.
   int k_src[kCopies], v_src[kCopies];
@@ -883,7 +887,8 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int key = key0 + 32 * j + 16 * kb + 4 * quad + e;
-              if (key > wave_row0 + 16 * qc + col) s.v[kb][qc][e] = -INFINITY;
+              if ((causal && key > wave_row0 + 16 * qc + col) || key >= S)
+                s.v[kb][qc][e] = -INFINITY;
             }
       };
       // Max of this lane's 8 raw scores of query block qc in a half. The
@@ -990,8 +995,9 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
           accumulate(1, p1);
         }
       };
-      // Only tiles crossing the diagonal are masked (a wave-uniform test).
-      if (causal && key0 + kTileKeys - 1 > wave_row0)
+      // Only tiles crossing the diagonal or the end of the keys are masked
+      // (a wave-uniform test).
+      if ((causal && key0 + kTileKeys - 1 > wave_row0) || key0 + kTileKeys > S)
         body(std::true_type{});
       else
         body(std::false_type{});
@@ -1101,7 +1107,8 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
         x.w += y.w;
       }
       const float4v xv = {x.x, x.y, x.z, x.w};
-      __builtin_nontemporal_store(xv, reinterpret_cast<float4v*>(obase + static_cast<std::size_t>(row) * D) + cc);
+      if (q0 + kRowsPerWave * bw + row < S)
+        __builtin_nontemporal_store(xv, reinterpret_cast<float4v*>(obase + static_cast<std::size_t>(row) * D) + cc);
     }
     return;
   }
@@ -1139,7 +1146,8 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
       const int row = kRowsPerStore * i + rr;
       const float4 x = stg[row * kChunks4 + (cc ^ (row % kChunks4))];
       const float4v xv = {x.x, x.y, x.z, x.w};
-      __builtin_nontemporal_store(xv, reinterpret_cast<float4v*>(obase + static_cast<std::size_t>(row) * D) + cc);
+      if (wave_row0 + row < S)
+        __builtin_nontemporal_store(xv, reinterpret_cast<float4v*>(obase + static_cast<std::size_t>(row) * D) + cc);
     }
   }
 }
@@ -1153,8 +1161,7 @@ inline bool f16_dma_ok(const void* q, const void* k, const void* v,
   // one head of K or V must be addressable with 32-bit buffer offsets
   const unsigned long long head_bytes =
       static_cast<unsigned long long>(sequence) * head_dim * 2ull;
-  return (head_dim == 64 || head_dim == 128) && sequence % kBlockRows == 0 &&
-         head_bytes < (1ull << 32) &&
+  return (head_dim == 64 || head_dim == 128) && head_bytes < (1ull << 32) &&
          opl::aligned16(q) && opl::aligned16(k) && opl::aligned16(v) &&
          opl::aligned16(out);
 }

@@ -460,7 +460,8 @@ def test_gemm_baseline_sizes(hip, dtype, size):
 # --------------------------------------------------------------------- attention
 
 # (S, D, causal, extreme): tests/attention_smoke.cu:168-173, edge shapes, and
-# shapes on this library's fp16 global->LDS path (D 64/128, S % 128 == 0).
+# shapes on this library's fp16 global->LDS path (D 64/128, aligned tensors:
+# offset 0).
 ATTN_SMALL = [(32, 64, False, False), (32, 128, True, False), (37, 71, True, True),
               (1, 1, False, False), (5, 16, True, False), (129, 32, True, False),
               (200, 96, False, False), (257, 128, True, False), (64, 40, False, False),
@@ -514,6 +515,26 @@ def test_attention_f16_fast_path_covers_every_block(hip, heads, s, d, causal):
     # 512 causal) split each block's keys between two wavefront groups of
     # the workgroup; larger ones do not.
     q, k, v = _attn_inputs(s, d, False, 970 + heads + s, heads=heads)
+    qb, kb, vb = (oracle.to_f16_bits(t) for t in (q, k, v))
+    ref = oracle.attention(*(oracle.from_f16_bits(t) for t in (qb, kb, vb)), causal)
+    y = hip.attention(qb, kb, vb, causal)
+    assert np.isfinite(y).all()
+    assert np.max(np.abs(y - ref)) <= 2e-3
+
+
+@pytest.mark.parametrize("heads,s,d,causal", [
+    # 64-row blocks (four key groups at D 128, two at D 64)
+    (1, 1, 128, False), (2, 33, 128, True), (3, 100, 128, False), (1, 1000, 128, True),
+    (12, 1000, 128, False), (3, 65, 64, True), (5, 1000, 64, False),
+    # D 128, 128-row blocks, keys split between two groups
+    (50, 300, 128, False), (100, 300, 128, True),
+    # 128-row blocks, keys not split
+    (260, 200, 128, False), (171, 383, 64, True), (129, 383, 64, False)])
+def test_attention_f16_fast_path_ragged_sequence(hip, heads, s, d, causal):
+    # S not a multiple of the query block: the last block's rows past S are
+    # computed from row S - 1 of Q and not stored, keys past S read zeros
+    # and are masked; every row up to S must be written and match the oracle.
+    q, k, v = _attn_inputs(s, d, False, 990 + heads + s, heads=heads)
     qb, kb, vb = (oracle.to_f16_bits(t) for t in (q, k, v))
     ref = oracle.attention(*(oracle.from_f16_bits(t) for t in (qb, kb, vb)), causal)
     y = hip.attention(qb, kb, vb, causal)
