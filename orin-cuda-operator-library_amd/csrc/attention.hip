@@ -20,7 +20,9 @@
 // attention_mfma_kernel (every other shape and fp32), which stages K / V
 // through registers.
 //
-// MI355X design, per 256-thread workgroup (4 wavefronts x 32 query rows):
+// MI355X design, per 256-thread workgroup (4 wavefronts x 32 query rows;
+// the register-staged kernel's lane layout, the fp16 fast path's is
+// described before it):
 //   * scores are computed transposed, S^T = K Q^T, so lane l of a wavefront
 //     owns query row (l % 32): its row max / row sum need only the lane's
 //     own registers plus one exchange with lane l ^ 32;
@@ -37,8 +39,8 @@
 //     diagonal / ragged tiles; workgroups are issued heaviest-first, and
 //     all workgroups of one head share an XCD (and its L2);
 //   * grids too small to fill the GPU split each query block's keys: the
-//     fp16 fast path between two wavefront groups of one workgroup (merged
-//     through LDS), the register-staged kernel over several workgroups
+//     fp16 fast path between two or four wavefront groups of one workgroup
+//     (merged through LDS), the register-staged kernel over several workgroups
 //     (partials in the stream's workspace, merged by
 //     attention_combine_kernel in split order).
 // Head dims are padded to a multiple of 32 with zeros (any 1 <= D <= 128).
