@@ -13,9 +13,29 @@
  * hipGetLastError().  Faults inside a kernel surface at the caller's next
  * synchronization, as with any asynchronous HIP work.
  *
+ * Device memory: the library never allocates. Launch sequences that need
+ * scratch beyond the caller's buffers (reduce partials, split-K partial
+ * sums, padded GEMM operands, split attention partials) take it from one
+ * of two places:
+ *   - the plain entry points: a static array of 64 MiB per GPU (the
+ *     "arena"), held from the library's load to process exit. Calls that
+ *     use it on different streams are ordered on the device by an event
+ *     chain, so they stay safe across streams and host threads without
+ *     blocking the host. A plan that would need more than 64 MiB uses
+ *     fewer splits or a kernel that needs none. Under stream capture the
+ *     chain is not captured: replays of such a graph must not overlap
+ *     another arena user on the same GPU (replay in stream order with the
+ *     other calls, or capture the *_ws entry points instead);
+ *   - the *_ws entry points: a workspace the caller passes (device memory,
+ *     256-byte aligned, at least the bytes the matching *_workspace_size
+ *     query returns for the same arguments, else hipErrorInvalidValue);
+ *     the caller orders its uses. With enough workspace the plan is the
+ *     one an unlimited arena would give.
+ *
  * The C++ API in operatorlib/operators.h (the drop-in for the reference's
- * include/operatorlib/operators.h:13-44) is a thin inline layer over these
- * symbols; the PyTorch binding calls that C++ layer.
+ * include/operatorlib/operators.h:13-44) is a thin inline layer over the
+ * plain entry points; the PyTorch binding calls the *_ws entry points with
+ * a workspace from torch's caching allocator.
  */
 #ifndef OPERATORLIB_OPERATORLIB_C_H_
 #define OPERATORLIB_OPERATORLIB_C_H_
@@ -31,7 +51,7 @@ extern "C" {
 typedef uint16_t operatorlib_half_t;
 
 /* Version of this ABI; bumped on any incompatible change. */
-#define OPERATORLIB_ABI_VERSION 1
+#define OPERATORLIB_ABI_VERSION 2
 int operatorlib_abi_version(void);
 
 /* Human-readable text for a status returned by any entry point. */
@@ -47,10 +67,26 @@ int operatorlib_reduce_sum_f32(const float* input, float* output, size_t n,
                                void* stream);
 
 /*
+ * Workspace form of operatorlib_reduce_sum_f32: the partials in `workspace`
+ * (see the top of this file). The result bits are those of
+ * operatorlib_reduce_sum_f32.
+ * Errors: as operatorlib_reduce_sum_f32; a workspace smaller than
+ * operatorlib_reduce_sum_f32_workspace_size(input, n), or NULL or not
+ * 256-byte aligned when that is non-zero.
+ * No counterpart in the reference (its launcher needs no scratch:
+ * src/reduce.cu:54-69): for callers that own all device memory.
+ */
+size_t operatorlib_reduce_sum_f32_workspace_size(const float* input, size_t n);
+int operatorlib_reduce_sum_f32_ws(const float* input, float* output, size_t n,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/*
  * operatorlib_reduce_sum_f32 without any allocation: the same kernels and
  * the same result bits, with the per-workgroup partials in a static device
- * array of 256 doubles (2 KiB per GPU, held until the process ends) instead
- * of library scratch. No hipMalloc, no hipFree, no allocating library call,
+ * array of its own, 256 doubles (2 KiB per GPU, held until the process
+ * ends), instead of the arena, and without the arena's host lock and event
+ * calls. No hipMalloc, no hipFree, no allocating library call,
  * on any call, so callers that cannot allocate (code under HIP graph
  * capture that forbids it, tight serving loops, harnesses that forbid
  * allocation) can use it. Any n is accepted: the grid is capped at 256
@@ -84,7 +120,9 @@ int operatorlib_transpose_f32(const float* input, float* output, int rows,
 /*
  * output[t, h] = input[t, h] * rsqrt(mean_h(input[t, :]^2) + epsilon)
  *                * weight[h]  for a row-major [tokens, hidden] input.
- * Errors: NULL pointer, tokens <= 0, hidden <= 0, epsilon <= 0 (or NaN).
+ * Errors: NULL pointer, tokens <= 0, hidden <= 0, epsilon <= 0 (the
+ * reference's `epsilon <= 0.0f` test, src/rmsnorm.cu:80-81: a NaN epsilon
+ * passes it and gives NaN rows).
  * Replaces operatorlib::rmsnorm_f32, reference src/rmsnorm.cu:77-95.
  */
 int operatorlib_rmsnorm_f32(const float* input, const float* weight,
@@ -134,6 +172,28 @@ int operatorlib_gemm_f16(const operatorlib_half_t* a,
                          int k, void* stream);
 
 /*
+ * Workspace forms of the GEMMs (see the top of this file): the query gives
+ * the scratch bytes of the plan for these operands (padded copies, split
+ * partial sums; 0 for most aligned shapes).
+ * Errors: as the plain forms; a workspace smaller than the query's answer,
+ * or NULL or not 256-byte aligned when that is non-zero.
+ * No counterpart in the reference (src/gemm.cu:440-479 needs no scratch):
+ * for callers that own all device memory.
+ */
+size_t operatorlib_gemm_f32_workspace_size(const float* a, const float* b,
+                                           int m, int n, int k);
+int operatorlib_gemm_f32_ws(const float* a, const float* b, float* c, int m,
+                            int n, int k, void* workspace,
+                            size_t workspace_bytes, void* stream);
+size_t operatorlib_gemm_f16_workspace_size(const operatorlib_half_t* a,
+                                           const operatorlib_half_t* b,
+                                           int m, int n, int k);
+int operatorlib_gemm_f16_ws(const operatorlib_half_t* a,
+                            const operatorlib_half_t* b, float* c, int m,
+                            int n, int k, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/*
  * output = softmax(Q K^T / sqrt(head_dim) [+ causal mask]) V for contiguous
  * [batch, heads, sequence, head_dim] fp32 tensors; causal != 0 hides key j
  * from query row i when j > i.
@@ -156,6 +216,39 @@ int operatorlib_attention_f16(const operatorlib_half_t* q,
                               const operatorlib_half_t* v, float* output,
                               int batch, int heads, int sequence,
                               int head_dim, int causal, void* stream);
+
+/*
+ * Workspace forms of the attention entry points (see the top of this
+ * file): key-split partials of small register-staged grids; the fp16 fast
+ * path (head_dim 64 or 128, 16-byte aligned tensors) needs none.
+ * Errors: as the plain forms; a workspace smaller than the query's answer,
+ * or NULL or not 256-byte aligned when that is non-zero. The queries
+ * return 0 for invalid arguments.
+ * No counterpart in the reference (src/attention.cu:445-507 needs no
+ * scratch): for callers that own all device memory.
+ */
+size_t operatorlib_attention_f32_workspace_size(const float* q, const float* k,
+                                                const float* v,
+                                                const float* output, int batch,
+                                                int heads, int sequence,
+                                                int head_dim, int causal);
+int operatorlib_attention_f32_ws(const float* q, const float* k,
+                                 const float* v, float* output, int batch,
+                                 int heads, int sequence, int head_dim,
+                                 int causal, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+size_t operatorlib_attention_f16_workspace_size(const operatorlib_half_t* q,
+                                                const operatorlib_half_t* k,
+                                                const operatorlib_half_t* v,
+                                                const float* output, int batch,
+                                                int heads, int sequence,
+                                                int head_dim, int causal);
+int operatorlib_attention_f16_ws(const operatorlib_half_t* q,
+                                 const operatorlib_half_t* k,
+                                 const operatorlib_half_t* v, float* output,
+                                 int batch, int heads, int sequence,
+                                 int head_dim, int causal, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -499,31 +499,48 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(
 constexpr long long kSplitBudget = 256;
 constexpr int kMaxSplits = 4;
 
+// Key splits of a register-staged call and the scratch bytes of their
+// partials: `splits` as above, fewer when the partials would not fit
+// `capacity` (one split needs none).
+struct SplitPlan {
+  int splits = 1;
+  std::size_t bytes = 0;
+};
+
 template <typename T, int NDT>
-hipError_t launch_attention(const T* q, const T* k, const T* v, float* out, int bh,
-                            int s, int d, int causal, bool vector_ok,
-                            hipStream_t stream) {
+SplitPlan split_plan(int bh, int s, int d, int causal, std::size_t capacity) {
   const int q_blocks = (s + kBlockRows - 1) / kBlockRows;
   const long long blocks = static_cast<long long>(q_blocks) * bh;
-  const float scale = 1.4426950408889634f / sqrtf(static_cast<float>(d));
   // Key tiles per query block bound the useful split count.
   const int max_tiles = (s + AttnLayout<T, NDT>::kKeys - 1) / AttnLayout<T, NDT>::kKeys;
   const long long budget = causal ? 2 * kSplitBudget : kSplitBudget;
   int splits = static_cast<int>(budget / blocks < kMaxSplits ? budget / blocks : kMaxSplits);
   if (splits > max_tiles) splits = max_tiles;
   if (splits < 1) splits = 1;
+  const std::size_t per_split =
+      static_cast<std::size_t>(bh) * s * (d + 2) * sizeof(float);
+  if (splits > 1 && static_cast<std::size_t>(splits) > capacity / per_split)
+    splits = static_cast<int>(capacity / per_split);
+  SplitPlan p;
+  p.splits = splits < 2 ? 1 : splits;
+  p.bytes = p.splits > 1 ? per_split * p.splits : 0;
+  return p;
+}
+
+// Runs the register-staged kernel; `scratch` holds plan.bytes.
+template <typename T, int NDT>
+hipError_t launch_attention(const T* q, const T* k, const T* v, float* out, int bh,
+                            int s, int d, int causal, bool vector_ok, const SplitPlan& plan,
+                            void* scratch, hipStream_t stream) {
+  const int q_blocks = (s + kBlockRows - 1) / kBlockRows;
+  const long long blocks = static_cast<long long>(q_blocks) * bh;
+  const float scale = 1.4426950408889634f / sqrtf(static_cast<float>(d));
+  const int splits = plan.splits;
   float* part_o = nullptr;
   float* part_ml = nullptr;
-  // Held until the combine kernel is enqueued (scratch.hpp).
-  std::optional<opl::ScratchLease> lease;
   if (splits > 1) {
     const std::size_t rows = static_cast<std::size_t>(bh) * s;
-    lease.emplace(stream);
-    opl::Scratch scratch;
-    const hipError_t status = lease->get(
-        static_cast<std::size_t>(splits) * rows * (d + 2) * sizeof(float), &scratch);
-    if (status != hipSuccess) return status;
-    part_o = static_cast<float*>(scratch.data);
+    part_o = static_cast<float*>(scratch);
     part_ml = part_o + static_cast<std::size_t>(splits) * rows * d;
   }
   const dim3 grid(static_cast<unsigned>(blocks * splits)), block(kThreads);
@@ -757,10 +774,14 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     k_src[j] = row * D + 8 * (phys ^ L::swizzle_k(row));
     v_src[j] = row * D + 8 * (phys ^ L::swizzle_v(row));
   }
-  // Buffer resources over this head's K and V (the launcher guarantees
-  // S * D * 2 < 2^32): the per-lane byte offsets stay in 32-bit VGPRs and
-  // the tile's position is a scalar offset, so a tile's copies cost no
-  // vector address arithmetic.
+  // Buffer resources over the rest of this head's K and V from the tile's
+  // first key (the launcher guarantees S * D * 2 < 2^32): the per-lane byte
+  // offsets stay in 32-bit VGPRs and the base is scalar, so a tile's copies
+  // cost no vector address arithmetic. The hardware range-checks only the
+  // per-lane offset against the resource's size (the scalar offset is
+  // exempt), so the tile's position goes into the base, not the scalar
+  // offset: keys from S on then fall outside the range and read zeros,
+  // never the next head or memory past the tensor.
   const unsigned head_bytes = static_cast<unsigned>(S) * D * 2u;
 #pragma unroll
   for (int j = 0; j < kCopies; ++j) {
@@ -772,16 +793,18 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   // costing a v_readfirstlane per copy and tile.
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto issue = [&](unsigned char* st, int key0) {
-    // < head_bytes < 2^32: unsigned, so a head above 2 GiB cannot overflow
+    // key0 < S for every issued tile, so 0 < rest <= head_bytes < 2^32
     const unsigned tile_bytes = static_cast<unsigned>(key0) * D * 2u;
+    const unsigned rest = head_bytes - tile_bytes;
+    const std::size_t tile_elems = static_cast<std::size_t>(key0) * D;
 #pragma unroll
     for (int j = 0; j < kCopies; ++j)
-      opl::buffer_copy16_lds(kh, head_bytes, st + (wave_s * kCopies + j) * 1024,
-                        k_src[j], tile_bytes);
+      opl::buffer_copy16_lds(kh + tile_elems, rest, st + (wave_s * kCopies + j) * 1024,
+                             k_src[j]);
 #pragma unroll
     for (int j = 0; j < kCopies; ++j)
-      opl::buffer_copy16_lds(vh, head_bytes, st + L::kTile + (wave_s * kCopies + j) * 1024,
-                        v_src[j], tile_bytes);
+      opl::buffer_copy16_lds(vh + tile_elems, rest,
+                             st + L::kTile + (wave_s * kCopies + j) * 1024, v_src[j]);
   };
   // K operand: key row col of each 16-key block, chunk 4 c + quad. Rows 16
   // apart share the swizzle, so the block and half offsets are immediates.
@@ -1171,6 +1194,7 @@ inline bool f16_dma_ok(const void* q, const void* k, const void* v,
 template <typename T>
 int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
                     int heads, int sequence, int head_dim, int causal,
+                    const opl::ScratchSource& src, std::size_t* query,
                     void* stream_handle) {
   if (!opl::attention_args_ok(q, k, v, out, batch, heads, sequence, head_dim))
     return hipErrorInvalidValue;
@@ -1186,6 +1210,10 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
   const int c = causal ? 1 : 0;
   if constexpr (sizeof(T) == 2) {
     if (f16_dma_ok(q, k, v, out, sequence, head_dim)) {
+      if (query != nullptr) {  // the fast path needs no scratch
+        *query = 0;
+        return hipSuccess;
+      }
       const float scale =
           1.4426950408889634f / sqrtf(static_cast<float>(head_dim));
       // Grids too small to fill the CUs split each query block's keys
@@ -1226,12 +1254,37 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
       return hipGetLastError();
     }
   }
-  switch ((head_dim + 31) / 32) {
-    case 1: return launch_attention<T, 1>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream);
-    case 2: return launch_attention<T, 2>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream);
-    case 3: return launch_attention<T, 3>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream);
-    default: return launch_attention<T, 4>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, stream);
+  const int ndt = (head_dim + 31) / 32;
+  SplitPlan plan;
+  switch (ndt) {
+    case 1: plan = split_plan<T, 1>(bh, sequence, head_dim, c, src.capacity()); break;
+    case 2: plan = split_plan<T, 2>(bh, sequence, head_dim, c, src.capacity()); break;
+    case 3: plan = split_plan<T, 3>(bh, sequence, head_dim, c, src.capacity()); break;
+    default: plan = split_plan<T, 4>(bh, sequence, head_dim, c, src.capacity()); break;
   }
+  if (query != nullptr) {
+    *query = plan.bytes;
+    return hipSuccess;
+  }
+  if (src.workspace_mode && !opl::workspace_ok(src.data, src.bytes, plan.bytes))
+    return hipErrorInvalidValue;
+  auto run = [&](void* scratch) -> hipError_t {
+    switch (ndt) {
+      case 1: return launch_attention<T, 1>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, plan, scratch, stream);
+      case 2: return launch_attention<T, 2>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, plan, scratch, stream);
+      case 3: return launch_attention<T, 3>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, plan, scratch, stream);
+      default: return launch_attention<T, 4>(q, k, v, out, bh, sequence, head_dim, c, vector_ok, plan, scratch, stream);
+    }
+  };
+  if (plan.bytes == 0) return run(nullptr);
+  // Held until the combine kernel is enqueued (scratch.hpp).
+  opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
+  if (lease.status() != hipSuccess) return lease.status();
+  return run(lease.data());
+}
+
+const _Float16* as_f16(const operatorlib_half_t* p) {
+  return reinterpret_cast<const _Float16*>(p);
 }
 
 }  // namespace
@@ -1241,8 +1294,8 @@ extern "C" int operatorlib_attention_f32(const float* q, const float* k,
                                          int batch, int heads, int sequence,
                                          int head_dim, int causal,
                                          void* stream_handle) {
-  return attention_entry<float>(q, k, v, output, batch, heads, sequence,
-                                head_dim, causal, stream_handle);
+  return attention_entry<float>(q, k, v, output, batch, heads, sequence, head_dim, causal,
+                                opl::ScratchSource{}, nullptr, stream_handle);
 }
 
 extern "C" int operatorlib_attention_f16(const operatorlib_half_t* q,
@@ -1251,9 +1304,58 @@ extern "C" int operatorlib_attention_f16(const operatorlib_half_t* q,
                                          float* output, int batch, int heads,
                                          int sequence, int head_dim,
                                          int causal, void* stream_handle) {
-  return attention_entry<_Float16>(reinterpret_cast<const _Float16*>(q),
-                                   reinterpret_cast<const _Float16*>(k),
-                                   reinterpret_cast<const _Float16*>(v),
-                                   output, batch, heads, sequence, head_dim,
-                                   causal, stream_handle);
+  return attention_entry<_Float16>(as_f16(q), as_f16(k), as_f16(v), output, batch, heads,
+                                   sequence, head_dim, causal, opl::ScratchSource{}, nullptr,
+                                   stream_handle);
+}
+
+// Workspace queries: the same plan as the call with these arguments,
+// nothing enqueued; invalid arguments report 0.
+extern "C" size_t operatorlib_attention_f32_workspace_size(const float* q, const float* k,
+                                                           const float* v,
+                                                           const float* output, int batch,
+                                                           int heads, int sequence,
+                                                           int head_dim, int causal) {
+  std::size_t bytes = 0;
+  if (attention_entry<float>(q, k, v, const_cast<float*>(output), batch, heads, sequence,
+                             head_dim, causal, opl::ScratchSource{true, nullptr, 0}, &bytes,
+                             nullptr) != hipSuccess)
+    return 0;
+  return bytes;
+}
+
+extern "C" size_t operatorlib_attention_f16_workspace_size(const operatorlib_half_t* q,
+                                                           const operatorlib_half_t* k,
+                                                           const operatorlib_half_t* v,
+                                                           const float* output, int batch,
+                                                           int heads, int sequence,
+                                                           int head_dim, int causal) {
+  std::size_t bytes = 0;
+  if (attention_entry<_Float16>(as_f16(q), as_f16(k), as_f16(v), const_cast<float*>(output),
+                                batch, heads, sequence, head_dim, causal,
+                                opl::ScratchSource{true, nullptr, 0}, &bytes,
+                                nullptr) != hipSuccess)
+    return 0;
+  return bytes;
+}
+
+extern "C" int operatorlib_attention_f32_ws(const float* q, const float* k, const float* v,
+                                            float* output, int batch, int heads, int sequence,
+                                            int head_dim, int causal, void* workspace,
+                                            size_t workspace_bytes, void* stream_handle) {
+  return attention_entry<float>(q, k, v, output, batch, heads, sequence, head_dim, causal,
+                                opl::ScratchSource{true, workspace, workspace_bytes}, nullptr,
+                                stream_handle);
+}
+
+extern "C" int operatorlib_attention_f16_ws(const operatorlib_half_t* q,
+                                            const operatorlib_half_t* k,
+                                            const operatorlib_half_t* v, float* output,
+                                            int batch, int heads, int sequence, int head_dim,
+                                            int causal, void* workspace, size_t workspace_bytes,
+                                            void* stream_handle) {
+  return attention_entry<_Float16>(as_f16(q), as_f16(k), as_f16(v), output, batch, heads,
+                                   sequence, head_dim, causal,
+                                   opl::ScratchSource{true, workspace, workspace_bytes}, nullptr,
+                                   stream_handle);
 }

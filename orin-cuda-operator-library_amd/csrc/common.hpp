@@ -161,19 +161,21 @@ __host__ __device__ inline bool aligned16(const void* p) {
 // parts: 32-bit data format, no index stride; only the byte range matters.
 constexpr int kBufferFlags = 0x00020000;
 
-// 16 bytes per lane from base + voffset + soffset into LDS at dst + 16 *
-// lane (dst wave-uniform), through a buffer resource over [base, base +
-// bytes): the base lives in scalar registers and a tile's position can be a
-// scalar offset, so a copy needs no 64-bit vector address arithmetic;
-// offsets past `bytes` read zeros. Kept out of kernel bodies so the host
-// compilation pass never meets the device-only resource type.
+// 16 bytes per lane from base + voffset into LDS at dst + 16 * lane (dst
+// wave-uniform), through a buffer resource over [base, base + bytes): the
+// base lives in scalar registers, so a copy needs no 64-bit vector address
+// arithmetic, and a lane whose offset reaches past `bytes` reads zeros and
+// touches no memory. The hardware range-checks only the per-lane offset,
+// not the instruction's scalar offset, so this helper passes no scalar
+// offset: callers move a tile's position into `base` and shrink `bytes` to
+// match. Kept out of kernel bodies so the host compilation pass never meets
+// the device-only resource type.
 __device__ __forceinline__ void buffer_copy16_lds(const void* base, unsigned bytes,
-                                                  unsigned char* dst, int voffset,
-                                                  int soffset) {
+                                                  unsigned char* dst, int voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
                                         bytes, kBufferFlags),
-      (__attribute__((address_space(3))) void*)dst, 16, voffset, soffset, 0, 0);
+      (__attribute__((address_space(3))) void*)dst, 16, voffset, 0, 0, 0);
 }
 
 // max / sum of v over lanes l and l ^ 32 (the two halves of a wavefront),

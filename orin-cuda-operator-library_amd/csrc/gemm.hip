@@ -133,7 +133,19 @@ struct LayoutFor<float> {
   using type = F32Layout;
 };
 
-template <typename T, bool kVector, typename L>
+// How gemm_mfma_kernel stages its operands from global memory:
+//   * kElementwise: element by element with zero fill (any shape and
+//     alignment);
+//   * kAligned16: one 16-byte load per chunk; rows are 16-byte aligned
+//     (K, N multiples of the chunk, 16-byte aligned A and B), so a chunk is
+//     wholly inside or outside a row;
+//   * kDword: one 16-byte load per chunk at 4-byte alignment (every fp32
+//     matrix; fp16 ones with even K and N and 4-byte aligned A and B); a
+//     chunk that runs past its row's end is loaded element by element, so
+//     no load reaches past a row (or the matrix).
+enum Staging { kElementwise, kAligned16, kDword };
+
+template <typename T, int kStaging, typename L>
 struct Stager {
   using P = Precision<T>;
   using Chunk = typename P::Chunk;
@@ -156,14 +168,24 @@ struct Stager {
                                                      int rows, int col,
                                                      int cols) {
     Chunk v;
-    if constexpr (kVector) {
-      // Vector instances need cols % E == 0, so a chunk is all in or out.
+    if constexpr (kStaging == kAligned16) {
+      // cols % E == 0, so a chunk is all in or out.
       if (row < rows && col < cols) {
         v = *reinterpret_cast<const Chunk*>(
             base + static_cast<std::size_t>(row) * ld + col);
       } else {
 #pragma unroll
         for (int e = 0; e < E; ++e) v[e] = T(0);
+      }
+    } else if constexpr (kStaging == kDword) {
+      typedef Chunk DwordChunk __attribute__((aligned(4)));
+      const T* p = base + static_cast<std::size_t>(row) * ld;
+      if (row < rows && col + E <= cols) {
+        v = *reinterpret_cast<const DwordChunk*>(p + col);
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          v[e] = (row < rows && col + e < cols) ? p[col + e] : T(0);
       }
     } else {
       const T* p = base + static_cast<std::size_t>(row) * ld;
@@ -266,14 +288,14 @@ __device__ __forceinline__ void super_tile_of_block(int tiles_n, int* tm, int* t
   *tn = (round % super_cols) * 16 + (x % 4) * 4 + q / 8;
 }
 
-template <typename T, bool kVector, typename L = typename LayoutFor<T>::type>
+template <typename T, int kStaging, typename L = typename LayoutFor<T>::type>
 __global__ __launch_bounds__(L::kThreads)
 __attribute__((amdgpu_waves_per_eu(L::kWavesPerSimd, L::kWavesPerSimd)))
 void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
                       float* __restrict__ C, int M, int N, int K, int ldb) {
   using P = Precision<T>;
   using Chunk = typename P::Chunk;
-  using S = Stager<T, kVector, L>;
+  using S = Stager<T, kStaging, L>;
   constexpr int kBM = L::kBM;
   constexpr int kBN = L::kBN;
   constexpr int kTileABytes = L::kTileABytes;
@@ -573,9 +595,9 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
 #pragma unroll
     for (int j = 0; j < kCopies; ++j) {
       opl::buffer_copy16_lds(a_base, a_span, stage + (wave * kCopies + j) * 1024,
-                             a_dma[j], 0);
+                             a_dma[j]);
       opl::buffer_copy16_lds(b_base, b_span, stage + kABytes + (wave * kCopies + j) * 1024,
-                             b_dma[j], 0);
+                             b_dma[j]);
     }
   };
 
@@ -1240,33 +1262,58 @@ bool applies(const T* b, int m, int n) {
   return m <= kMaxM && n % Cfg<T>::kPerLane == 0 && opl::aligned16(b);
 }
 
+// K split of one call: `splits` workgroup rows of `chunk` K rows each (a
+// multiple of 32, at most kMaxChunk, the A rows one workgroup stages), and
+// the scratch bytes of their partial sums (0 for one split).
+struct Plan {
+  int splits = 1;
+  int chunk = 0;
+  std::size_t bytes = 0;
+  bool ok = false;  // false: no split fits `capacity`
+};
+
+inline Plan plan_with(int m, int n, int k, int splits) {
+  Plan p;
+  int chunk = (k + splits - 1) / splits;
+  chunk = (chunk + 31) / 32 * 32;
+  if (chunk > kMaxChunk) chunk = kMaxChunk;
+  p.chunk = chunk;
+  p.splits = (k + chunk - 1) / chunk;
+  p.bytes = p.splits > 1 ? static_cast<std::size_t>(p.splits) * m * n * sizeof(float) : 0;
+  p.ok = true;
+  return p;
+}
+
+// Enough workgroups to cover the GPU about twice, as scratch allows: fewer
+// splits when their partials would not fit `capacity`, none of this kernel
+// when even the fewest (K / kMaxChunk) would not.
 template <typename T>
-hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k,
-                  hipStream_t stream) {
-  using C = Cfg<T>;
-  const int blocks_n = (n + C::kBlockN - 1) / C::kBlockN;
-  // Enough workgroups to cover the GPU about twice; chunks of at most
-  // kMaxChunk rows, a multiple of 32.
+Plan plan(int m, int n, int k, std::size_t capacity) {
+  const int blocks_n = (n + Cfg<T>::kBlockN - 1) / Cfg<T>::kBlockN;
   int splits = (512 + blocks_n - 1) / blocks_n;
   const int max_splits = (k + 63) / 64;
   if (splits > max_splits) splits = max_splits;
   if (splits < 1) splits = 1;
-  int chunk = (k + splits - 1) / splits;
-  chunk = (chunk + 31) / 32 * 32;
-  if (chunk > kMaxChunk) chunk = kMaxChunk;
-  splits = (k + chunk - 1) / chunk;
-  float* dst = c;
-  // Held until the split sum is enqueued (scratch.hpp).
-  std::optional<opl::ScratchLease> lease;
-  if (splits > 1) {
-    lease.emplace(stream);
-    opl::Scratch scratch;
-    const hipError_t status = lease->get(
-        static_cast<std::size_t>(splits) * m * n * sizeof(float), &scratch);
-    if (status != hipSuccess) return status;
-    dst = static_cast<float*>(scratch.data);
-  }
-  const dim3 grid(static_cast<unsigned>(blocks_n), static_cast<unsigned>(splits));
+  Plan p = plan_with(m, n, k, splits);
+  if (p.bytes <= capacity) return p;
+  const std::size_t per_split = static_cast<std::size_t>(m) * n * sizeof(float);
+  const std::size_t fit = capacity / per_split;
+  const int fewest = (k + kMaxChunk - 1) / kMaxChunk;
+  if (fit < static_cast<std::size_t>(fewest)) return Plan{};
+  p = plan_with(m, n, k, static_cast<int>(fit < static_cast<std::size_t>(splits) ? fit : splits));
+  p.ok = p.bytes <= capacity;
+  return p;
+}
+
+// Runs plan `p` (p.ok); `partials` holds p.bytes of scratch when p.splits > 1.
+template <typename T>
+hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k, const Plan& p,
+                  void* partials, hipStream_t stream) {
+  using C = Cfg<T>;
+  const int blocks_n = (n + C::kBlockN - 1) / C::kBlockN;
+  float* dst = p.splits > 1 ? static_cast<float*>(partials) : c;
+  const int chunk = p.chunk;
+  const dim3 grid(static_cast<unsigned>(blocks_n), static_cast<unsigned>(p.splits));
   if (m >= C::kMfmaMinM) {
     const bool vec_a =
         k % kLaneRows == 0 &&
@@ -1280,11 +1327,11 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k,
   else if (m <= 4) launch_m<T, 4>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 8) launch_m<T, 8>(a, b, dst, m, n, k, chunk, grid, stream);
   else launch_m<T, 16>(a, b, dst, m, n, k, chunk, grid, stream);
-  if (splits > 1) {
+  if (p.splits > 1) {
     const long long count = static_cast<long long>(m) * n;
     const long long blocks = (count + kSumThreads - 1) / kSumThreads;
     sum_splits_kernel<<<dim3(static_cast<unsigned>(blocks < 16384 ? blocks : 16384)),
-                        dim3(kSumThreads), 0, stream>>>(dst, c, count, splits);
+                        dim3(kSumThreads), 0, stream>>>(dst, c, count, p.splits);
   }
   return hipGetLastError();
 }
@@ -1361,14 +1408,38 @@ void launch_pad_copy(const T* src, int rows, int cols, T* dst, int rows_p,
 
 inline long long round_up(long long x, long long to) { return (x + to - 1) / to * to; }
 
-// Large GEMMs whose operands miss the fast kernels' rules (K or N not a
-// multiple of the chunk / K step, or unaligned pointers; the 4095^3 edge
-// case) are run on zero-padded aligned copies: the copies cost a few
-// percent of the product at these sizes, the element-wise general kernel
-// several times more. Zero rows/columns of K contribute nothing; padded
-// columns of N are never stored.
+// Large fp16 GEMMs whose operands miss the direct-to-LDS kernel's rules (K
+// not a multiple of its K step, N not a multiple of 8, or operands not
+// 16-byte aligned; the 4095^3 edge case) run it on zero-padded aligned
+// copies when the copies fit the call's scratch: the copies cost a few
+// percent of the product at these sizes, the element-wise register-staged
+// kernel several times more. Zero rows/columns of K contribute nothing;
+// padded columns of N are never stored. (fp32 never pads: its rows are
+// always 4-byte aligned, which the kDword staging reads directly.)
 inline bool worth_padding(int m, int n, int k) {
   return m >= 128 && n >= 128 && 2.0 * m * n * static_cast<double>(k) >= 1073741824.0;
+}
+
+// The padded copies of one call: A as [m, kp] and/or B as [kp, np], A's
+// copy first in scratch, B's at a 256-byte boundary after it.
+struct PadPlan {
+  bool pad_a = false, pad_b = false;
+  long long kp = 0, np = 0;
+  std::size_t a_bytes = 0, b_bytes = 0;
+  std::size_t bytes() const { return a_bytes + b_bytes; }
+};
+
+template <typename T>
+PadPlan pad_plan(const T* a, const T* b, int m, int n, int k, int k_mult, int n_mult) {
+  PadPlan p;
+  p.kp = round_up(k, k_mult);
+  p.np = round_up(n, n_mult);
+  p.pad_a = p.kp != k || !opl::aligned16(a);
+  p.pad_b = p.kp != k || p.np != n || !opl::aligned16(b);
+  if (p.pad_a)
+    p.a_bytes = static_cast<std::size_t>(round_up(static_cast<long long>(m) * p.kp * sizeof(T), 256));
+  if (p.pad_b) p.b_bytes = static_cast<std::size_t>(p.kp * p.np * sizeof(T));
+  return p;
 }
 
 struct PaddedOperands {
@@ -1378,49 +1449,37 @@ struct PaddedOperands {
   int ldb;  // row stride of B
 };
 
-// Pads A to [m, kp] and/or B to [kp, np] in library scratch as needed. The
-// caller keeps `lease` until the product that reads the copies is enqueued.
+// Enqueues the copies of plan `pp` into `ws` (pp.bytes() of scratch).
 template <typename T>
-hipError_t pad_operands(const T* a, const T* b, int m, int n, int k, int k_mult,
-                        int n_mult, hipStream_t stream, opl::ScratchLease& lease,
-                        PaddedOperands* out) {
-  const long long kp = round_up(k, k_mult);
-  const long long np = round_up(n, n_mult);
-  const bool pad_a = kp != k || !opl::aligned16(a);
-  const bool pad_b = kp != k || np != n || !opl::aligned16(b);
-  if (kp > 0x7fffffffLL || np > 0x7fffffffLL) return hipErrorInvalidValue;
-  const std::size_t a_bytes =
-      pad_a ? static_cast<std::size_t>(round_up(static_cast<long long>(m) * kp * sizeof(T), 256)) : 0;
-  const std::size_t b_bytes = pad_b ? static_cast<std::size_t>(kp * np * sizeof(T)) : 0;
-  opl::Scratch scratch;
-  hipError_t status = lease.get(a_bytes + b_bytes, &scratch);
-  if (status != hipSuccess) return status;
-  void* ws = scratch.data;
+PaddedOperands pad_into(const T* a, const T* b, int m, int n, int k, const PadPlan& pp,
+                        void* ws, hipStream_t stream) {
   T* pa = static_cast<T*>(ws);
-  T* pb = reinterpret_cast<T*>(static_cast<unsigned char*>(ws) + a_bytes);
-  if (pad_a) launch_pad_copy<T>(a, m, k, pa, m, static_cast<int>(kp), stream);
-  if (pad_b)
-    launch_pad_copy<T>(b, k, n, pb, static_cast<int>(kp), static_cast<int>(np), stream);
-  out->a = pad_a ? static_cast<const void*>(pa) : a;
-  out->b = pad_b ? static_cast<const void*>(pb) : b;
-  out->k = static_cast<int>(kp);
-  out->ldb = pad_b ? static_cast<int>(np) : n;
-  return hipGetLastError();
+  T* pb = reinterpret_cast<T*>(static_cast<unsigned char*>(ws) + pp.a_bytes);
+  if (pp.pad_a) launch_pad_copy<T>(a, m, k, pa, m, static_cast<int>(pp.kp), stream);
+  if (pp.pad_b)
+    launch_pad_copy<T>(b, k, n, pb, static_cast<int>(pp.kp), static_cast<int>(pp.np), stream);
+  PaddedOperands out;
+  out.a = pp.pad_a ? static_cast<const void*>(pa) : a;
+  out.b = pp.pad_b ? static_cast<const void*>(pb) : b;
+  out.k = static_cast<int>(pp.kp);
+  out.ldb = pp.pad_b ? static_cast<int>(pp.np) : n;
+  return out;
 }
 
-// One launch of gemm_mfma_kernel with tile layout L (general or 16-byte
-// vector staging).
+// One launch of gemm_mfma_kernel with tile layout L and staging `staging`.
 template <typename T, typename L>
-hipError_t launch_generic(bool vector, const T* a, const T* b, float* c, int m,
+hipError_t launch_generic(int staging, const T* a, const T* b, float* c, int m,
                           int n, int k, int ldb, hipStream_t stream) {
   const long long tiles = static_cast<long long>((m + L::kBM - 1) / L::kBM) *
                           ((n + L::kBN - 1) / L::kBN);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(tiles)), block(L::kThreads);
-  if (vector)
-    gemm_mfma_kernel<T, true, L><<<grid, block, 0, stream>>>(a, b, c, m, n, k, ldb);
+  if (staging == kAligned16)
+    gemm_mfma_kernel<T, kAligned16, L><<<grid, block, 0, stream>>>(a, b, c, m, n, k, ldb);
+  else if (staging == kDword)
+    gemm_mfma_kernel<T, kDword, L><<<grid, block, 0, stream>>>(a, b, c, m, n, k, ldb);
   else
-    gemm_mfma_kernel<T, false, L><<<grid, block, 0, stream>>>(a, b, c, m, n, k, ldb);
+    gemm_mfma_kernel<T, kElementwise, L><<<grid, block, 0, stream>>>(a, b, c, m, n, k, ldb);
   return hipGetLastError();
 }
 
@@ -1433,34 +1492,27 @@ hipError_t launch_generic(bool vector, const T* a, const T* b, float* c, int m,
 constexpr long long kSmallGridTilesF32 = 256;
 
 template <typename T>
-hipError_t launch_generic_for(bool vector, const T* a, const T* b, float* c, int m,
+hipError_t launch_generic_for(int staging, const T* a, const T* b, float* c, int m,
                               int n, int k, int ldb, hipStream_t stream) {
   using L = typename LayoutFor<T>::type;
   if constexpr (std::is_same<T, float>::value) {
     const long long big_tiles = static_cast<long long>((m + L::kBM - 1) / L::kBM) *
                                 ((n + L::kBN - 1) / L::kBN);
     if (big_tiles < kSmallGridTilesF32)
-      return launch_generic<T, F32SmallLayout>(vector, a, b, c, m, n, k, ldb, stream);
+      return launch_generic<T, F32SmallLayout>(staging, a, b, c, m, n, k, ldb, stream);
   }
-  return launch_generic<T, L>(vector, a, b, c, m, n, k, ldb, stream);
+  return launch_generic<T, L>(staging, a, b, c, m, n, k, ldb, stream);
 }
 
+// The fastest staging the operands allow (Staging above).
 template <typename T>
-hipError_t launch_gemm(const T* a, const T* b, float* c, int m, int n, int k,
-                       hipStream_t stream) {
+int staging_for(const T* a, const T* b, int n, int k) {
   constexpr int E = Precision<T>::kChunkElems;
-  const bool vector_ok = k % E == 0 && n % E == 0 && opl::aligned16(a) &&
-                         opl::aligned16(b);
-  if (vector_ok) return launch_generic_for<T>(true, a, b, c, m, n, k, n, stream);
-  if (worth_padding(m, n, k)) {
-    opl::ScratchLease lease(stream);
-    PaddedOperands p;
-    const hipError_t status = pad_operands<T>(a, b, m, n, k, E, E, stream, lease, &p);
-    if (status != hipSuccess) return status;
-    return launch_generic_for<T>(true, static_cast<const T*>(p.a),
-                                 static_cast<const T*>(p.b), c, m, n, p.k, p.ldb, stream);
-  }
-  return launch_generic_for<T>(false, a, b, c, m, n, k, n, stream);
+  if (k % E == 0 && n % E == 0 && opl::aligned16(a) && opl::aligned16(b)) return kAligned16;
+  const bool dword_rows = k * sizeof(T) % 4 == 0 && n * sizeof(T) % 4 == 0 &&
+                          reinterpret_cast<std::uintptr_t>(a) % 4 == 0 &&
+                          reinterpret_cast<std::uintptr_t>(b) % 4 == 0;
+  return dword_rows ? kDword : kElementwise;
 }
 
 template <typename Cfg>
@@ -1492,13 +1544,13 @@ hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
 // A 256 x 256-tile grid that fills R >= 1 rounds of one workgroup per CU
 // plus a last round at most half full leaves most CUs idle for a whole
 // tile's time: the last round's tiles are then split along K into enough
-// parts to fill the CUs (at most 16, at least 256 deep each) and summed
-// by a second launch. Measured on MI355X (us, unsplit vs split): 4096 x
-// 4160 x 4096 (272 tiles, 16 in the last round: 16 parts of 4 K steps)
-// 180-185 vs 138-143; 4160 x 4096 x 4032 (15 uneven parts) 184 vs 145;
-// 4100 x 4104 x 2048 (289 tiles, 33 last: 7 parts) 101 vs 93. Last
-// rounds more than half full stay unsplit (4096 x 11008: 688 tiles, 176
-// last).
+// parts to fill the CUs (at most 16, at least 256 deep each, and as many as
+// their partial tiles fit the call's scratch) and summed by a second
+// launch. Measured on MI355X (us, unsplit vs split): 4096 x 4160 x 4096 (272
+// tiles, 16 in the last round: 16 parts of 4 K steps) 180-185 vs 138-143;
+// 4160 x 4096 x 4032 (15 uneven parts) 184 vs 145; 4100 x 4104 x 2048 (289
+// tiles, 33 last: 7 parts) 101 vs 93. Last rounds more than half full stay
+// unsplit (4096 x 11008: 688 tiles, 176 last).
 constexpr int kTailMaxSplits = 16;
 constexpr int kTailMinDepth = 256;
 
@@ -1516,38 +1568,41 @@ int device_cus() {
 // 4096 (180) 102.8 vs 110.0; 4096^3 (256) 121.1 vs 136.5.
 constexpr long long kSmallGridTiles = 160;
 
-// 256 x 256 tiles (Big: BigTile or BigTileK32), the last round split
-// along K when it is at most half full.
-template <typename Big>
-hipError_t launch_big_tiles(const _Float16* a, const _Float16* b, float* c, int m, int n,
-                            int k, int ldb, long long big_tiles, hipStream_t stream,
-                            bool may_split_tail) {
-  const int cus = may_split_tail ? device_cus() : 0;
+// Split of the last round of a 256 x 256-tile grid (splits == 0: none).
+struct TailPlan {
+  int splits = 0;
+  long long last = 0;  // tiles in the last round
+  std::size_t bytes = 0;
+};
+
+TailPlan tail_plan(int m, int n, int k, std::size_t capacity) {
+  TailPlan t;
+  const long long big_tiles =
+      static_cast<long long>((m + dma::BigTile::kBM - 1) / dma::BigTile::kBM) *
+      ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
+  if (big_tiles < kSmallGridTiles) return t;
+  const int cus = device_cus();
   const long long last = cus > 0 ? big_tiles % cus : 0;
-  if (cus > 0 && big_tiles > cus && last > 0 && last <= cus / 2) {
-    int splits = static_cast<int>(cus / last);
-    if (splits > kTailMaxSplits) splits = kTailMaxSplits;
-    if (splits > k / kTailMinDepth) splits = k / kTailMinDepth;
-    if (splits >= 2) {
-      opl::ScratchLease lease(stream);
-      if (lease.status() != hipSuccess) return lease.status();
-      opl::Scratch scratch;
-      const std::size_t bytes =
-          static_cast<std::size_t>(last) * splits * Big::kBM * Big::kBN * sizeof(float);
-      const hipError_t status = lease.get(bytes, &scratch);
-      if (status != hipSuccess) return status;
-      const dma::TailSplit tail{static_cast<int>(big_tiles - last), static_cast<int>(last),
-                                splits, static_cast<float*>(scratch.data)};
-      return launch_dma_tiles<Big>(a, b, c, m, n, k, ldb, stream, tail);
-    }
-  }
-  return launch_dma_tiles<Big>(a, b, c, m, n, k, ldb, stream);
+  if (cus <= 0 || big_tiles <= cus || last == 0 || last > cus / 2) return t;
+  const std::size_t per_split =
+      static_cast<std::size_t>(last) * dma::BigTile::kBM * dma::BigTile::kBN * sizeof(float);
+  long long splits = cus / last;
+  if (splits > kTailMaxSplits) splits = kTailMaxSplits;
+  if (splits > k / kTailMinDepth) splits = k / kTailMinDepth;
+  if (static_cast<std::size_t>(splits) > capacity / per_split)
+    splits = static_cast<long long>(capacity / per_split);
+  if (splits < 2) return t;
+  t.splits = static_cast<int>(splits);
+  t.last = last;
+  t.bytes = per_split * static_cast<std::size_t>(splits);
+  return t;
 }
 
-// k % dma::kBK == 0.
+// The direct-to-LDS kernel (k % dma::kBK == 0) on 128 x 128 or 256 x 256
+// tiles, with `tail` split into `partials` (tail.bytes of scratch).
 hipError_t launch_gemm_f16_dma(const _Float16* a, const _Float16* b, float* c,
-                               int m, int n, int k, int ldb, hipStream_t stream,
-                               bool may_split_tail) {
+                               int m, int n, int k, int ldb, const TailPlan& tail,
+                               void* partials, hipStream_t stream) {
   static_assert(dma::BigTile::kBM == dma::BigTileK32::kBM &&
                     dma::BigTile::kBN == dma::BigTileK32::kBN,
                 "one big tile size");
@@ -1556,11 +1611,105 @@ hipError_t launch_gemm_f16_dma(const _Float16* a, const _Float16* b, float* c,
       ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
   if (big_tiles < kSmallGridTiles)
     return launch_dma_tiles<dma::SmallTile>(a, b, c, m, n, k, ldb, stream);
+  dma::TailSplit split{0, 0, 0, nullptr};
+  if (tail.splits > 0)
+    split = dma::TailSplit{static_cast<int>(big_tiles - tail.last), static_cast<int>(tail.last),
+                           tail.splits, static_cast<float*>(partials)};
   if (k % dma::BigTile::kBK == 0)
-    return launch_big_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, big_tiles, stream,
-                                          may_split_tail);
-  return launch_big_tiles<dma::BigTileK32>(a, b, c, m, n, k, ldb, big_tiles, stream,
-                                           may_split_tail);
+    return launch_dma_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, stream, split);
+  return launch_dma_tiles<dma::BigTileK32>(a, b, c, m, n, k, ldb, stream, split);
+}
+
+// One call's plan and the scratch it needs.
+struct GemmPlan {
+  enum Kind { kSkinny, kDma, kPaddedDma, kRegister } kind = kRegister;
+  skinny::Plan skinny;
+  TailPlan tail;  // kDma
+  PadPlan pad;    // kPaddedDma
+  int staging = kElementwise;  // kRegister
+  std::size_t bytes = 0;
+};
+
+template <typename T>
+GemmPlan plan_gemm(const T* a, const T* b, int m, int n, int k, std::size_t capacity) {
+  GemmPlan p;
+  if (skinny::applies(b, m, n)) {
+    p.skinny = skinny::plan<T>(m, n, k, capacity);
+    if (p.skinny.ok) {
+      p.kind = GemmPlan::kSkinny;
+      p.bytes = p.skinny.bytes;
+      return p;
+    }
+  }
+  if constexpr (std::is_same<T, _Float16>::value) {
+    // The copy kernel's per-lane offsets inside a tile are 32-bit: up to
+    // 255 rows of A (255 * K * 2 bytes) and 64 rows of B (64 * N * 2).
+    const bool dma_offsets_fit = k < (1 << 22) && n < (1 << 24);
+    if (dma_offsets_fit && k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
+        opl::aligned16(b)) {
+      p.kind = GemmPlan::kDma;
+      p.tail = tail_plan(m, n, k, capacity);
+      p.bytes = p.tail.bytes;
+      return p;
+    }
+    if (dma_offsets_fit && worth_padding(m, n, k)) {
+      const PadPlan pad = pad_plan<T>(a, b, m, n, k, dma::kBK, 8);
+      if (pad.kp <= 0x7fffffffLL && pad.np <= 0x7fffffffLL && pad.bytes() <= capacity) {
+        p.kind = GemmPlan::kPaddedDma;
+        p.pad = pad;
+        p.bytes = pad.bytes();
+        return p;
+      }
+    }
+  }
+  p.kind = GemmPlan::kRegister;
+  p.staging = staging_for<T>(a, b, n, k);
+  return p;
+}
+
+// Runs plan `p`; `scratch` holds p.bytes (unused when 0).
+template <typename T>
+hipError_t run_gemm(const GemmPlan& p, const T* a, const T* b, float* c, int m, int n, int k,
+                    void* scratch, hipStream_t stream) {
+  switch (p.kind) {
+    case GemmPlan::kSkinny:
+      return skinny::launch<T>(a, b, c, m, n, k, p.skinny, scratch, stream);
+    case GemmPlan::kDma:
+    case GemmPlan::kPaddedDma:
+      if constexpr (std::is_same<T, _Float16>::value) {
+        if (p.kind == GemmPlan::kDma)
+          return launch_gemm_f16_dma(a, b, c, m, n, k, n, p.tail, scratch, stream);
+        const PaddedOperands q = pad_into<T>(a, b, m, n, k, p.pad, scratch, stream);
+        return launch_gemm_f16_dma(static_cast<const T*>(q.a), static_cast<const T*>(q.b), c,
+                                   m, n, q.k, q.ldb, TailPlan{}, nullptr, stream);
+      }
+      return hipErrorInvalidValue;
+    default:
+      return launch_generic_for<T>(p.staging, a, b, c, m, n, k, n, stream);
+  }
+}
+
+// A GEMM call with its scratch from `src`; query != nullptr only reports the
+// plan's scratch bytes (nothing is enqueued).
+template <typename T>
+int gemm_entry(const T* a, const T* b, float* c, int m, int n, int k,
+               const opl::ScratchSource& src, std::size_t* query, hipStream_t stream) {
+  const GemmPlan p = plan_gemm<T>(a, b, m, n, k, src.capacity());
+  if (query != nullptr) {
+    *query = p.bytes;
+    return hipSuccess;
+  }
+  if (src.workspace_mode && !opl::workspace_ok(src.data, src.bytes, p.bytes))
+    return hipErrorInvalidValue;
+  if (p.bytes == 0) return run_gemm<T>(p, a, b, c, m, n, k, nullptr, stream);
+  // Held until the last kernel that reads the scratch is enqueued.
+  opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
+  if (lease.status() != hipSuccess) return lease.status();
+  return run_gemm<T>(p, a, b, c, m, n, k, lease.data(), stream);
+}
+
+const _Float16* as_f16(const operatorlib_half_t* p) {
+  return reinterpret_cast<const _Float16*>(p);
 }
 
 }  // namespace
@@ -1569,9 +1718,8 @@ extern "C" int operatorlib_gemm_f32(const float* a, const float* b, float* c,
                                     int m, int n, int k,
                                     void* stream_handle) {
   if (!opl::gemm_args_ok(a, b, c, m, n, k)) return hipErrorInvalidValue;
-  hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-  if (skinny::applies(b, m, n)) return skinny::launch<float>(a, b, c, m, n, k, stream);
-  return launch_gemm<float>(a, b, c, m, n, k, stream);
+  return gemm_entry<float>(a, b, c, m, n, k, opl::ScratchSource{}, nullptr,
+                           static_cast<hipStream_t>(stream_handle));
 }
 
 extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
@@ -1579,26 +1727,43 @@ extern "C" int operatorlib_gemm_f16(const operatorlib_half_t* a,
                                     int m, int n, int k,
                                     void* stream_handle) {
   if (!opl::gemm_args_ok(a, b, c, m, n, k)) return hipErrorInvalidValue;
-  const _Float16* ha = reinterpret_cast<const _Float16*>(a);
-  const _Float16* hb = reinterpret_cast<const _Float16*>(b);
-  hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-  if (skinny::applies(hb, m, n)) return skinny::launch<_Float16>(ha, hb, c, m, n, k, stream);
-  // The copy kernel's per-lane offsets inside a tile are 32-bit: up to
-  // 255 rows of A (255 * K * 2 bytes) and 64 rows of B (64 * N * 2).
-  const bool dma_offsets_fit = k < (1 << 22) && n < (1 << 24);
-  if (dma_offsets_fit && k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
-      opl::aligned16(b))
-    return launch_gemm_f16_dma(ha, hb, c, m, n, k, n, stream, true);
-  if (dma_offsets_fit && worth_padding(m, n, k)) {
-    opl::ScratchLease lease(stream);
-    PaddedOperands p;
-    const hipError_t status =
-        pad_operands<_Float16>(ha, hb, m, n, k, dma::kBK, 8, stream, lease, &p);
-    if (status != hipSuccess) return status;
-    // (the lease above already holds this stream's scratch: no tail split)
-    return launch_gemm_f16_dma(static_cast<const _Float16*>(p.a),
-                               static_cast<const _Float16*>(p.b), c, m, n, p.k,
-                               p.ldb, stream, false);
-  }
-  return launch_gemm<_Float16>(ha, hb, c, m, n, k, stream);
+  return gemm_entry<_Float16>(as_f16(a), as_f16(b), c, m, n, k, opl::ScratchSource{}, nullptr,
+                              static_cast<hipStream_t>(stream_handle));
+}
+
+extern "C" size_t operatorlib_gemm_f32_workspace_size(const float* a, const float* b, int m,
+                                                      int n, int k) {
+  if (!opl::gemm_args_ok(a, b, a, m, n, k)) return 0;
+  std::size_t bytes = 0;
+  gemm_entry<float>(a, b, nullptr, m, n, k, opl::ScratchSource{true, nullptr, 0}, &bytes,
+                    nullptr);
+  return bytes;
+}
+
+extern "C" size_t operatorlib_gemm_f16_workspace_size(const operatorlib_half_t* a,
+                                                      const operatorlib_half_t* b, int m,
+                                                      int n, int k) {
+  if (!opl::gemm_args_ok(a, b, a, m, n, k)) return 0;
+  std::size_t bytes = 0;
+  gemm_entry<_Float16>(as_f16(a), as_f16(b), nullptr, m, n, k,
+                       opl::ScratchSource{true, nullptr, 0}, &bytes, nullptr);
+  return bytes;
+}
+
+extern "C" int operatorlib_gemm_f32_ws(const float* a, const float* b, float* c, int m, int n,
+                                       int k, void* workspace, size_t workspace_bytes,
+                                       void* stream_handle) {
+  if (!opl::gemm_args_ok(a, b, c, m, n, k)) return hipErrorInvalidValue;
+  return gemm_entry<float>(a, b, c, m, n, k,
+                           opl::ScratchSource{true, workspace, workspace_bytes}, nullptr,
+                           static_cast<hipStream_t>(stream_handle));
+}
+
+extern "C" int operatorlib_gemm_f16_ws(const operatorlib_half_t* a, const operatorlib_half_t* b,
+                                       float* c, int m, int n, int k, void* workspace,
+                                       size_t workspace_bytes, void* stream_handle) {
+  if (!opl::gemm_args_ok(a, b, c, m, n, k)) return hipErrorInvalidValue;
+  return gemm_entry<_Float16>(as_f16(a), as_f16(b), c, m, n, k,
+                              opl::ScratchSource{true, workspace, workspace_bytes}, nullptr,
+                              static_cast<hipStream_t>(stream_handle));
 }

@@ -11,14 +11,15 @@
 //     register, so rounding error stays far below the fp32 result ulp even
 //     for ill-conditioned (zero-mean) inputs; a wave64 DPP/permlane fp64
 //     reduction and an 8-slot LDS combine give one fp64 partial per
-//     workgroup, written to library scratch (scratch.hpp);
+//     workgroup, written to scratch: the caller's workspace
+//     (operatorlib_reduce_sum_f32_ws) or the GPU's arena (scratch.hpp);
 //   * pass 2: one workgroup adds the partials in index order and writes the
 //     fp32 result (stream order makes pass 1's partials visible).
 // Inputs that fit one workgroup skip pass 2. No memset, no float atomics.
 //
 // operatorlib_reduce_sum_f32_noalloc runs the same two kernels with the
-// partials in a file-scope device array (`scratch`, 2 KiB per GPU) instead
-// of library scratch, so it never allocates.
+// partials in a file-scope device array of its own (`scratch`, 2 KiB per
+// GPU), with no lease: no cross-stream ordering, no host lock.
 //
 // Why two launches: combining in the same launch needs each workgroup to
 // publish its partial at device scope and count arrivals. With a release
@@ -185,20 +186,47 @@ hipError_t scratch_on_current_device(double** out) {
   return hipSuccess;
 }
 
+// Scratch bytes of a plan: one fp64 partial per pass-1 workgroup when there
+// is more than one.
+std::size_t partial_bytes(const Plan& p) {
+  return p.blocks > 1 ? sizeof(double) * static_cast<std::size_t>(p.blocks) : 0;
+}
+
+// The partials come from the caller's workspace (src.workspace_mode) or the
+// arena; either way a plan needs at most 2 KiB, so every plan fits and the
+// result bits do not depend on the scratch source.
+int reduce_with(const float* input, float* output, std::size_t n,
+                const opl::ScratchSource& src, hipStream_t stream) {
+  const Plan p = plan_for(input, n);
+  const std::size_t bytes = partial_bytes(p);
+  if (src.workspace_mode && !opl::workspace_ok(src.data, src.bytes, bytes))
+    return hipErrorInvalidValue;
+  if (bytes == 0) return enqueue(input, output, n, p, nullptr, stream);
+  // Held until the combine kernel is enqueued (scratch.hpp).
+  opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
+  if (lease.status() != hipSuccess) return lease.status();
+  return enqueue(input, output, n, p, static_cast<double*>(lease.data()), stream);
+}
+
 }  // namespace
 
 extern "C" int operatorlib_reduce_sum_f32(const float* input, float* output,
                                           size_t n, void* stream_handle) {
   if (!opl::reduce_args_ok(input, output, n)) return hipErrorInvalidValue;
-  hipStream_t stream = static_cast<hipStream_t>(stream_handle);
-  const Plan p = plan_for(input, n);
-  if (p.blocks == 1) return enqueue(input, output, n, p, nullptr, stream);
-  // Held until the combine kernel is enqueued (scratch.hpp).
-  opl::ScratchLease lease(stream);
-  opl::Scratch partials;
-  const hipError_t status = lease.get(sizeof(double) * kGridBlocks, &partials);
-  if (status != hipSuccess) return status;
-  return enqueue(input, output, n, p, static_cast<double*>(partials.data), stream);
+  return reduce_with(input, output, n, opl::ScratchSource{},
+                     static_cast<hipStream_t>(stream_handle));
+}
+
+extern "C" size_t operatorlib_reduce_sum_f32_workspace_size(const float* input, size_t n) {
+  return n == 0 ? 0 : partial_bytes(plan_for(input, n));
+}
+
+extern "C" int operatorlib_reduce_sum_f32_ws(const float* input, float* output, size_t n,
+                                             void* workspace, size_t workspace_bytes,
+                                             void* stream_handle) {
+  if (!opl::reduce_args_ok(input, output, n)) return hipErrorInvalidValue;
+  return reduce_with(input, output, n, opl::ScratchSource{true, workspace, workspace_bytes},
+                     static_cast<hipStream_t>(stream_handle));
 }
 
 extern "C" int operatorlib_reduce_sum_f32_noalloc(const float* input, float* output,

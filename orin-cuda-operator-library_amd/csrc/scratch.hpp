@@ -1,46 +1,44 @@
 #pragma once
-// Library-owned device scratch and the lease that serialises its users.
+// Device scratch for the launch sequences that need memory beyond the
+// caller's buffers, and the lease that hands it out. The library never
+// allocates device memory: scratch is either the caller's workspace or a
+// fixed static array per GPU.
 //
-// Some launch sequences need device memory beyond the caller's buffers:
-//   * reduce: one fp64 partial per workgroup, summed by a second launch;
-//   * decode GEMMs (M <= 16): split-K partial sums, summed by a second
-//     launch;
-//   * GEMMs whose operands miss the fast kernels' shape / alignment rules:
-//     zero-padded aligned operand copies;
-//   * fp16 GEMMs whose last round of 256x256 tiles fills at most half the
-//     CUs: split-K partial tiles of that round, summed by a second launch;
-//   * register-staged attention on small grids: per-split partial outputs,
-//     merged by a second launch.
+// Users (each sizes its plan to the scratch it is offered; less scratch
+// means fewer splits or a slower kernel, never an error):
+//   * reduce: one fp64 partial per workgroup (at most 2 KiB);
+//   * decode GEMMs (M <= 16): split-K partial sums;
+//   * fp16 GEMMs whose operands miss the direct-to-LDS kernel's shape or
+//     alignment rules: zero-padded operand copies;
+//   * fp16 GEMMs whose last round of 256 x 256 tiles fills at most half the
+//     CUs: split-K partial tiles of that round;
+//   * register-staged attention on small grids: per-split partials.
 // The reference launchers need none of this (src/reduce.cu:54-69 combines
 // with float atomics after an in-stream memset) and are reentrant because
-// they share nothing; this library keeps the reentrancy as follows.
+// they share nothing.
 //
-// Scratch is kept per (device, stream key). The stream key is the stream
-// handle, except that hipStreamPerThread names a different stream in every
-// host thread, so its key also holds the thread. A ScratchLease locks the
-// key's scratch from construction to destruction; a launcher constructs one
-// before its first enqueue that touches the scratch and keeps it until its
-// last such enqueue has returned. Two host threads that launch on one stream
-// (the null stream included) therefore enqueue their sequences one after the
-// other, never interleaved, and stream order then keeps the device work of
-// one sequence from overlapping the next.
-//
-// Eager buffers grow on demand: a request larger than the key's buffer
-// allocates a new one of max(request, 2 x current) and retires the old one
-// without freeing it (kernels earlier in the stream may still read it, and
-// freeing would synchronize), so memory per key stays under twice its
-// largest request. Buffers live until process exit.
-//
-// Under stream capture the lease never touches the stream's eager buffer:
-// each request gets a buffer of its own, allocated with the thread's capture
-// mode switched to relaxed for the allocation (hipMalloc does not enqueue on
-// the capturing stream). The graph's kernels
-// then own that memory: eager calls on the capture stream, or on the stream
-// the graph is replayed on, can run concurrently with a replay without
-// sharing scratch. Two replays of one graph that overlap in time share it,
-// as with any graph that holds intermediate buffers. Capture-private
-// buffers are kept until process exit (a graph's lifetime is not visible
-// to the library).
+// Where scratch comes from:
+//   * a caller workspace (the *_ws entry points of the C ABI): the caller
+//     owns it and orders its uses on its streams; the lease only hands it
+//     out. The torch binding passes a tensor from torch's stream-ordered,
+//     capture-aware caching allocator here;
+//   * otherwise the device arena: a static __device__ array of kArenaBytes,
+//     one per GPU, held from the library's load to process exit. Every
+//     stream of a GPU shares it, so a lease on the arena
+//       - holds that GPU's host mutex while the sequence is enqueued,
+//       - makes the stream wait (hipStreamWaitEvent) for the end of the
+//         previous arena sequence when that one ran on another stream,
+//       - records the end of its own sequence in the GPU's event.
+//     Arena sequences therefore run one after another on the device,
+//     whatever streams and host threads issue them, and nothing blocks the
+//     host. Library-held device memory is kArenaBytes per GPU (plus the
+//     no-allocation reduce's 2 KiB), whatever the number of calls, streams
+//     or captured graphs.
+//   * under stream capture the arena's event chain is left out of the
+//     graph: a replay uses the arena without waiting for other arena users.
+//     Replays must therefore not overlap another arena sequence on the same
+//     GPU (replay in stream order with the other calls that use it), or the
+//     capturing caller passes a workspace (the torch binding always does).
 
 #include <hip/hip_runtime.h>
 
@@ -48,31 +46,58 @@
 
 namespace opl {
 
-struct Scratch {
-  void* data = nullptr;  // >= the requested bytes, 256-byte aligned
-};
+// Bytes of each GPU's arena. It holds the padded operands of an fp16 GEMM
+// up to 4096 x 4096 x 4096 and every other BASELINE-size plan in full.
+constexpr std::size_t kArenaBytes = std::size_t(64) << 20;
+
+// Plans are computed for a scratch capacity: kUnlimited for workspace-size
+// queries and the *_ws entry points, kArenaBytes for the others.
+constexpr std::size_t kUnlimited = ~std::size_t(0);
 
 class ScratchLease {
  public:
-  // Locks the scratch of `stream` on the current device (eager streams) or
-  // notes that `stream` is capturing. Check status() before get().
-  explicit ScratchLease(hipStream_t stream);
+  // workspace != nullptr: the caller's [workspace, workspace + bytes).
+  // Otherwise the current device's arena (locked for the lease's lifetime).
+  // Check status() before data().
+  ScratchLease(hipStream_t stream, void* workspace, std::size_t bytes);
   ~ScratchLease();
   ScratchLease(const ScratchLease&) = delete;
   ScratchLease& operator=(const ScratchLease&) = delete;
 
   hipError_t status() const { return status_; }
+  // 256-byte aligned.
+  void* data() const { return data_; }
+  std::size_t capacity() const { return capacity_; }
 
-  // Scratch of at least `bytes`.
-  hipError_t get(std::size_t bytes, Scratch* out);
-
-  struct Entry;  // one key's buffer and lock (scratch.hip)
+  struct Device;  // one GPU's arena state (scratch.hip)
 
  private:
   hipStream_t stream_;
   hipError_t status_ = hipSuccess;
+  void* data_ = nullptr;
+  std::size_t capacity_ = 0;
   bool capturing_ = false;
-  Entry* entry_ = nullptr;
+  Device* device_ = nullptr;
 };
+
+// Where a call's scratch comes from. Workspace mode (the *_ws entry points
+// and the workspace-size queries): plans assume unlimited capacity and the
+// entry point checks the caller's workspace against the plan. Otherwise the
+// arena, and plans fit kArenaBytes.
+struct ScratchSource {
+  bool workspace_mode = false;
+  void* data = nullptr;
+  std::size_t bytes = 0;
+  std::size_t capacity() const { return workspace_mode ? kUnlimited : kArenaBytes; }
+};
+
+// Checks a *_ws call's workspace against the bytes its plan needs: enough
+// bytes, and a 256-byte aligned pointer (every torch allocation is) when
+// any are needed.
+inline bool workspace_ok(const void* workspace, std::size_t bytes, std::size_t needed) {
+  if (needed == 0) return true;
+  return workspace != nullptr && bytes >= needed &&
+         (reinterpret_cast<std::size_t>(workspace) & 255u) == 0;
+}
 
 }  // namespace opl

@@ -15,7 +15,9 @@
 // tensors (HIP device memory on one device, dense row-major, one dtype from
 // the operator's set); extent() turns a tensor size into the int the C ABI
 // takes; launch() runs one C ABI call under a device guard on the current
-// stream. Each operator then states only its own shape rules.
+// stream. Each operator then states only its own shape rules. Operators
+// whose kernels may need scratch (reduce_sum, gemm, attention) call the
+// *_ws entry points with a Workspace from torch's allocator.
 
 #include <ATen/ATen.h>
 #include <ATen/hip/HIPContext.h>
@@ -23,6 +25,7 @@
 #include <torch/library.h>
 
 #include <cmath>
+#include <cstddef>
 #include <cstdint>
 #include <initializer_list>
 #include <limits>
@@ -100,6 +103,23 @@ std::pair<int, int> rows_by_last(const Operands& in, const at::Tensor& t,
 
 const void* caddr(const at::Tensor& t) { return t.data_ptr(); }
 
+// Scratch for a *_ws entry point: `bytes` from torch's caching allocator on
+// the inputs' device, handed back to it when the operator returns. The
+// allocator is stream-ordered (the block is reused only by later work on
+// the current stream, which is where the call's kernels run) and
+// capture-aware (under graph capture it comes from the graph's pool), so
+// the library itself holds no memory for these calls.
+struct Workspace {
+  at::Tensor tensor;
+  Workspace(const Operands& in, std::size_t bytes) {
+    if (bytes > 0)
+      tensor = at::empty({static_cast<std::int64_t>(bytes)},
+                         in.lead().options().dtype(at::kByte));
+  }
+  void* data() const { return tensor.defined() ? tensor.data_ptr() : nullptr; }
+  std::size_t bytes() const { return tensor.defined() ? tensor.numel() : 0; }
+};
+
 // Runs `call(stream)` (one C ABI entry point) with the inputs' device
 // current, on that device's current stream.
 template <typename Call>
@@ -117,9 +137,11 @@ at::Tensor reduce_sum_op(const at::Tensor& input) {
   TORCH_CHECK(input.numel() > 0, "reduce_sum: input must not be empty");
   at::Tensor out = at::empty({}, input.options());
   launch(in, [&](void* s) {
-    return operatorlib_reduce_sum_f32(static_cast<const float*>(caddr(input)),
-                                      static_cast<float*>(out.data_ptr()),
-                                      static_cast<size_t>(input.numel()), s);
+    const float* x = static_cast<const float*>(caddr(input));
+    const size_t n = static_cast<size_t>(input.numel());
+    const Workspace ws(in, operatorlib_reduce_sum_f32_workspace_size(x, n));
+    return operatorlib_reduce_sum_f32_ws(x, static_cast<float*>(out.data_ptr()), n,
+                                         ws.data(), ws.bytes(), s);
   });
   return out;
 }
@@ -196,12 +218,16 @@ at::Tensor gemm_op(const at::Tensor& a, const at::Tensor& b) {
   at::Tensor out = at::empty({m, n}, a.options().dtype(at::kFloat));
   launch(in, [&](void* s) {
     float* c = static_cast<float*>(out.data_ptr());
-    return in.half()
-               ? operatorlib_gemm_f16(static_cast<const operatorlib_half_t*>(caddr(a)),
-                                      static_cast<const operatorlib_half_t*>(caddr(b)),
-                                      c, m, n, k, s)
-               : operatorlib_gemm_f32(static_cast<const float*>(caddr(a)),
-                                      static_cast<const float*>(caddr(b)), c, m, n, k, s);
+    if (in.half()) {
+      const auto* ha = static_cast<const operatorlib_half_t*>(caddr(a));
+      const auto* hb = static_cast<const operatorlib_half_t*>(caddr(b));
+      const Workspace ws(in, operatorlib_gemm_f16_workspace_size(ha, hb, m, n, k));
+      return operatorlib_gemm_f16_ws(ha, hb, c, m, n, k, ws.data(), ws.bytes(), s);
+    }
+    const auto* fa = static_cast<const float*>(caddr(a));
+    const auto* fb = static_cast<const float*>(caddr(b));
+    const Workspace ws(in, operatorlib_gemm_f32_workspace_size(fa, fb, m, n, k));
+    return operatorlib_gemm_f32_ws(fa, fb, c, m, n, k, ws.data(), ws.bytes(), s);
   });
   return out;
 }
@@ -226,16 +252,22 @@ at::Tensor attention_op(const at::Tensor& q, const at::Tensor& k,
   launch(in, [&](void* s) {
     float* o = static_cast<float*>(out.data_ptr());
     const int c = causal ? 1 : 0;
-    return in.half()
-               ? operatorlib_attention_f16(
-                     static_cast<const operatorlib_half_t*>(caddr(q)),
-                     static_cast<const operatorlib_half_t*>(caddr(k)),
-                     static_cast<const operatorlib_half_t*>(caddr(v)), o, batch, heads,
-                     seq, dim, c, s)
-               : operatorlib_attention_f32(static_cast<const float*>(caddr(q)),
-                                           static_cast<const float*>(caddr(k)),
-                                           static_cast<const float*>(caddr(v)), o, batch,
-                                           heads, seq, dim, c, s);
+    if (in.half()) {
+      const auto* hq = static_cast<const operatorlib_half_t*>(caddr(q));
+      const auto* hk = static_cast<const operatorlib_half_t*>(caddr(k));
+      const auto* hv = static_cast<const operatorlib_half_t*>(caddr(v));
+      const Workspace ws(in, operatorlib_attention_f16_workspace_size(hq, hk, hv, o, batch,
+                                                                      heads, seq, dim, c));
+      return operatorlib_attention_f16_ws(hq, hk, hv, o, batch, heads, seq, dim, c,
+                                          ws.data(), ws.bytes(), s);
+    }
+    const auto* fq = static_cast<const float*>(caddr(q));
+    const auto* fk = static_cast<const float*>(caddr(k));
+    const auto* fv = static_cast<const float*>(caddr(v));
+    const Workspace ws(in, operatorlib_attention_f32_workspace_size(fq, fk, fv, o, batch,
+                                                                    heads, seq, dim, c));
+    return operatorlib_attention_f32_ws(fq, fk, fv, o, batch, heads, seq, dim, c, ws.data(),
+                                        ws.bytes(), s);
   });
   return out;
 }

@@ -32,9 +32,12 @@ inline bool matrix_args_ok(const void* input, const void* output, int rows,
 inline bool rmsnorm_args_ok(const void* input, const void* weight,
                             const void* output, int tokens, int hidden,
                             float epsilon) {
-  // `epsilon > 0` is false for NaN, so NaN is rejected as in the reference.
+  // The reference's own predicate, `epsilon <= 0.0f` rejects
+  // (src/rmsnorm.cu:80-81): NaN compares false, so a NaN epsilon is accepted
+  // and gives NaN rows, as there. (The torch binding rejects non-finite
+  // epsilon before it gets here, as the reference's binding does.)
   return input != nullptr && weight != nullptr && output != nullptr &&
-         tokens > 0 && hidden > 0 && epsilon > 0.0f;
+         tokens > 0 && hidden > 0 && !(epsilon <= 0.0f);
 }
 
 inline bool gemm_args_ok(const void* a, const void* b, const void* c, int m,

@@ -59,6 +59,36 @@ C_SYMBOLS = {
     "operatorlib_attention_f16": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_void_p,
                                              _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
                                              _c.c_void_p]),
+    # workspace forms: the caller's device memory instead of the GPU's arena
+    "operatorlib_reduce_sum_f32_workspace_size": (_c.c_size_t, [_c.c_void_p, _c.c_size_t]),
+    "operatorlib_reduce_sum_f32_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_size_t,
+                                                 _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "operatorlib_gemm_f32_workspace_size": (_c.c_size_t, [_c.c_void_p, _c.c_void_p, _c.c_int,
+                                                          _c.c_int, _c.c_int]),
+    "operatorlib_gemm_f32_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int,
+                                           _c.c_int, _c.c_int, _c.c_void_p, _c.c_size_t,
+                                           _c.c_void_p]),
+    "operatorlib_gemm_f16_workspace_size": (_c.c_size_t, [_c.c_void_p, _c.c_void_p, _c.c_int,
+                                                          _c.c_int, _c.c_int]),
+    "operatorlib_gemm_f16_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int,
+                                           _c.c_int, _c.c_int, _c.c_void_p, _c.c_size_t,
+                                           _c.c_void_p]),
+    "operatorlib_attention_f32_workspace_size": (_c.c_size_t, [_c.c_void_p, _c.c_void_p,
+                                                               _c.c_void_p, _c.c_void_p,
+                                                               _c.c_int, _c.c_int, _c.c_int,
+                                                               _c.c_int, _c.c_int]),
+    "operatorlib_attention_f32_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p,
+                                                _c.c_void_p, _c.c_int, _c.c_int, _c.c_int,
+                                                _c.c_int, _c.c_int, _c.c_void_p, _c.c_size_t,
+                                                _c.c_void_p]),
+    "operatorlib_attention_f16_workspace_size": (_c.c_size_t, [_c.c_void_p, _c.c_void_p,
+                                                               _c.c_void_p, _c.c_void_p,
+                                                               _c.c_int, _c.c_int, _c.c_int,
+                                                               _c.c_int, _c.c_int]),
+    "operatorlib_attention_f16_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p,
+                                                _c.c_void_p, _c.c_int, _c.c_int, _c.c_int,
+                                                _c.c_int, _c.c_int, _c.c_void_p, _c.c_size_t,
+                                                _c.c_void_p]),
 }
 
 _clib = None

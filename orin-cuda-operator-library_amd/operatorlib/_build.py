@@ -46,7 +46,7 @@ COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
 
 LIB_SOURCES = [
     "reduce.hip", "softmax.hip", "rmsnorm.hip", "transpose.hip",
-    "gemm.hip", "attention.hip", "scratch.cpp", "capi.cpp",
+    "gemm.hip", "attention.hip", "scratch.hip", "capi.cpp",
 ]
 
 LIBRARY = LIB_DIR / "liboperatorlib.so"

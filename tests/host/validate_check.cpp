@@ -75,13 +75,14 @@ int main() {
   for (const std::size_t n : sizes)
     expect(opl::reduce_args_ok(p, p, n), n != 0, "reduce n", static_cast<long long>(n % LLONG_MAX), 0);
 
-  // epsilon: strictly positive; NaN and -0.0 are rejected, +inf accepted
-  // (the reference's `epsilon <= 0.0f` test has the same outcomes).
+  // epsilon: the reference's `epsilon <= 0.0f` rejection test
+  // (src/rmsnorm.cu:80-81): zero, -0.0 and negatives are rejected; NaN
+  // compares false there, so it is accepted, as is +inf.
   const float nan = std::numeric_limits<float>::quiet_NaN();
   const float eps[] = {nan, -nan, -1.0f, -0.0f, 0.0f,
                        std::numeric_limits<float>::denorm_min(), 1e-6f,
                        std::numeric_limits<float>::infinity()};
-  const bool eps_ok[] = {false, false, false, false, false, true, true, true};
+  const bool eps_ok[] = {true, true, false, false, false, true, true, true};
   for (int i = 0; i < 8; ++i)
     expect(opl::rmsnorm_args_ok(p, p, p, 2, 2, eps[i]), eps_ok[i], "rmsnorm eps", i, 0);
 

@@ -69,7 +69,8 @@ def test_reduce_pins_and_determinism(hip):
 
 
 def test_reduce_two_streams(lib):
-    """Concurrent reduces on two streams use separate scratch."""
+    """Reduces on two streams at once share the GPU's arena: its event
+    chain orders them on the device, and both sums stay right."""
     from gpu_util import ptr, stream_handle, to_device
     xs = [oracle.uniform(40 + i, 3_000_000) for i in range(2)]
     ds = [to_device(x) for x in xs]
@@ -242,6 +243,19 @@ def test_rmsnorm_matches_oracle(hip, shape, eps, offset):
 
 def test_rmsnorm_pins(hip):
     pins.pin_rmsnorm(hip.rmsnorm, tol=3e-7)
+
+
+def test_rmsnorm_nan_epsilon_is_accepted_as_in_the_reference(lib):
+    # The reference launcher rejects only `epsilon <= 0.0f`
+    # (src/rmsnorm.cu:80-81), which is false for NaN: the call succeeds and
+    # every output is NaN (rsqrt of NaN).
+    x = to_device(oracle.normal(61, (3, 40)))
+    w = to_device(oracle.uniform(62, 40, 0.5, 1.5))
+    out = empty((3, 40))
+    check(lib.operatorlib_rmsnorm_f32(ptr(x), ptr(w), ptr(out), 3, 40, float("nan"),
+                                      stream_handle()), "rmsnorm")
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all()
 
 
 # -------------------------------------------------------------------------- gemm
@@ -421,8 +435,8 @@ def test_gemm_f16_step_counts(hip, mnk):
 
 
 def test_gemm_padded_then_smaller(hip):
-    """The per-stream workspace is reused: a large padded call followed by a
-    smaller one (and a larger one, which grows it) must all be right."""
+    """The arena is reused: a large padded call followed by a smaller one
+    and a larger one must all be right."""
     for m, n, k in [(1200, 1100, 1001), (700, 800, 1999), (1500, 1500, 1500)]:
         a = oracle.uniform(630 + m, (m, k))
         b = oracle.uniform(631 + n, (k, n))
@@ -439,12 +453,25 @@ def test_gemm_pins(hip):
     pins.pin_gemm(f16)  # every pin input is exactly representable in fp16
 
 
+def tile_row_rows(size: int, seed: int, tile: int = 256) -> np.ndarray:
+    """A seeded row inside every `tile`-row band of C, both rows at every band
+    boundary, and the first and last rows: every 256 x 256 tile row of the
+    GEMM grid (and, since rows are compared whole, every tile) is checked."""
+    rng = np.random.default_rng(seed)
+    rows = {0, size - 1}
+    for t0 in range(0, size, tile):
+        rows.add(int(t0 + rng.integers(0, min(tile, size - t0))))
+        if t0 > 0:
+            rows.update({t0 - 1, t0})
+    return np.array(sorted(rows), dtype=np.int32)
+
+
 @pytest.mark.parametrize("dtype,size", [("f32", 4096), ("f32", 4095), ("f16", 4096),
                                         ("f16", 4095), ("f16", 8192)])
 def test_gemm_baseline_sizes(hip, dtype, size):
     a = oracle.uniform(800 + size, (size, size))
     b = oracle.uniform(801 + size, (size, size))
-    rows = sample_rows(size, 14, 802)
+    rows = tile_row_rows(size, 802)
     if dtype == "f16":
         a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
         y = hip.gemm_f16(a, b)
@@ -542,27 +569,74 @@ def test_attention_f16_fast_path_ragged_sequence(hip, heads, s, d, causal):
     assert np.max(np.abs(y - ref)) <= 2e-3
 
 
+# (heads, S, D, causal) on every fp16 fast-path instance with S ragged:
+# D 128 64-row blocks / 128-row blocks with keys split / unsplit, D 64
+# 64-row blocks / 128-row blocks.
+POISON_CASES = [(1, 300, 128, False), (2, 1000, 128, True), (50, 300, 128, False),
+                (20, 1000, 128, True), (100, 300, 128, False), (70, 1000, 128, True),
+                (1, 1000, 64, True), (3, 300, 64, False), (200, 300, 64, True),
+                (60, 1000, 64, False)]
+
+
+@pytest.mark.parametrize("heads,s,d,causal", POISON_CASES)
+def test_attention_f16_reads_no_key_past_the_sequence(lib, heads, s, d, causal):
+    # Q, K and V end one 64-key tile before the end of an allocation whose
+    # tail holds NaN. The last key tile of every head runs past S; its keys
+    # from S on must read zeros (a read of the next head's rows or of the
+    # NaN tail would turn P.V into NaN, since masked p = 0 times NaN is NaN).
+    q, k, v = _attn_inputs(s, d, False, 1100 + heads + s, heads=heads)
+    bits = [oracle.to_f16_bits(t) for t in (q, k, v)]
+    tail = 64 * d
+
+    def poisoned(b):
+        flat = torch.full((b.size + tail,), float("nan"), dtype=torch.float16, device="cuda")
+        flat[:b.size].copy_(torch.from_numpy(b.reshape(-1).view(np.float16)).to("cuda"))
+        return flat
+
+    dq, dk, dv = (poisoned(b) for b in bits)
+    out = empty((1, heads, s, d))
+    check(lib.operatorlib_attention_f16(ptr(dq), ptr(dk), ptr(dv), ptr(out), 1, heads, s,
+                                        d, int(causal), stream_handle()), "attention_f16")
+    torch.cuda.synchronize()
+    y = out.cpu().numpy().astype(np.float64).reshape(heads, s, d)
+    assert np.isfinite(y).all()
+    # the last head in full, plus seeded rows of the others
+    rng = np.random.default_rng(1101)
+    hs = np.concatenate([np.full(s, heads - 1), rng.integers(0, heads, 256)]).astype(np.int32)
+    rs = np.concatenate([np.arange(s), rng.integers(0, s, 256)]).astype(np.int32)
+    ref = oracle.attention(*(oracle.from_f16_bits(b) for b in bits), causal, hs, rs)
+    assert np.max(np.abs(y[hs, rs] - ref)) <= 2e-3
+
+
 def test_attention_pins(hip):
     pins.pin_attention(hip.attention, tol=2e-6)
     f16 = lambda q, k, v, c: hip.attention(*(oracle.to_f16_bits(t) for t in (q, k, v)), c)
     pins.pin_attention(f16, tol=1e-2)
 
 
-@pytest.mark.parametrize("b,h,s,causal,rows", [(1, 12, 1024, False, 768),
-                                               (1, 12, 1024, True, 768),
-                                               (4, 32, 8192, True, 160)])
-def test_attention_f16_baseline(hip, b, h, s, causal, rows):
+@pytest.mark.parametrize("b,h,s,causal", [(1, 12, 1024, False), (1, 12, 1024, True),
+                                          (4, 32, 8192, True)])
+def test_attention_f16_baseline(hip, b, h, s, causal):
     d = 128
     q, k, v = (oracle.to_f16_bits(oracle.normal(1000 + i, (b, h, s, d))) for i in range(3))
     y = hip.attention(q, k, v, causal)
     qf, kf, vf = (oracle.from_f16_bits(t) for t in (q, k, v))
+    if s <= 1024:  # every row
+        ref = oracle.attention(qf, kf, vf, causal)
+        assert np.max(np.abs(y - ref)) <= 2e-3
+        return
+    # One seeded row in every (head, 128-row query block) work item of the
+    # fast path, plus in every head the first and last rows and both rows at
+    # the edges of the first query block's diagonal tile (SURVEY-scale
+    # sample: 128 x 64 + 128 x 8 = 9216 rows).
     rng = np.random.default_rng(1001)
-    heads = rng.integers(0, b * h, rows).astype(np.int32)
-    rws = rng.integers(0, s, rows).astype(np.int32)
-    # always include the first/last rows and the diagonal tile edges
-    extra_rows = np.array([0, 1, 127, 128, s - 1, s - 2], np.int32)
-    heads = np.concatenate([heads, np.zeros(6, np.int32), np.full(6, b * h - 1, np.int32)])
-    rws = np.concatenate([rws, extra_rows, extra_rows])
+    blocks = s // 128
+    heads = np.repeat(np.arange(b * h, dtype=np.int32), blocks)
+    rws = (np.tile(np.arange(blocks, dtype=np.int32) * 128, b * h) +
+           rng.integers(0, 128, b * h * blocks).astype(np.int32))
+    edges = np.array([0, 1, 63, 64, 127, 128, s - 2, s - 1], np.int32)
+    heads = np.concatenate([heads, np.repeat(np.arange(b * h, dtype=np.int32), edges.size)])
+    rws = np.concatenate([rws, np.tile(edges, b * h)])
     ref = oracle.attention(qf, kf, vf, causal, heads, rws)
     got = y.reshape(b * h, s, d)[heads, rws]
     assert np.max(np.abs(got - ref)) <= 2e-3

@@ -62,7 +62,7 @@ def lib():
 
 def test_every_declared_symbol_is_exported(lib):
     names = declared_c_functions()
-    assert len(names) == 13, names
+    assert len(names) == 23, names
     assert set(names) == set(operatorlib.C_SYMBOLS)
     for name in names:
         assert hasattr(lib, name), name
@@ -80,7 +80,7 @@ def test_exported_dynamic_symbols_are_exactly_the_abi():
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.operatorlib_abi_version() == 1
+    assert lib.operatorlib_abi_version() == 2
     assert lib.operatorlib_status_string(0)
     assert b"invalid" in lib.operatorlib_status_string(INVALID).lower()
 
@@ -127,7 +127,7 @@ def test_matrix_ops_reject(lib, fn, args):
     (NULL, FAKE, FAKE, 2, 8, 1e-5), (FAKE, NULL, FAKE, 2, 8, 1e-5), (FAKE, FAKE, NULL, 2, 8, 1e-5),
     (FAKE, FAKE, FAKE, 0, 8, 1e-5), (FAKE, FAKE, FAKE, 2, 0, 1e-5),
     (FAKE, FAKE, FAKE, 2, 8, 0.0), (FAKE, FAKE, FAKE, 2, 8, -1e-5),
-    (FAKE, FAKE, FAKE, 2, 8, float("nan"))])
+    (FAKE, FAKE, FAKE, 2, 8, -0.0), (FAKE, FAKE, FAKE, 2, 8, float("-inf"))])
 @pytest.mark.parametrize("fn", ["operatorlib_rmsnorm_f32", "operatorlib_rmsnorm_f16"])
 def test_rmsnorm_rejects(lib, fn, args):
     assert getattr(lib, fn)(*args, NULL) == INVALID
@@ -187,3 +187,57 @@ def test_bench_refuses_more_than_one_gpu():
     assert proc.returncode == 2
     assert "--gpus 2 is not supported" in proc.stdout + proc.stderr
     assert not proc.stdout.strip().startswith("{")  # no bench line
+
+
+# ------------------------------------------------------------- workspace forms
+# Queries and the *_ws entry points' workspace checks run before any HIP
+# call, so they are exercised here with fake (never dereferenced) pointers.
+# The shapes avoid the fp16 direct-to-LDS path, whose plan reads the CU
+# count from the runtime.
+
+def test_reduce_workspace_size(lib):
+    q = lib.operatorlib_reduce_sum_f32_workspace_size
+    assert q(FAKE, 0) == 0
+    assert q(FAKE, 100) == 0                      # one workgroup: no partials
+    assert q(FAKE, 1_000_003) == 8 * 123          # 250,000 float4 / 2048 per workgroup
+    assert q(FAKE, 1 << 24) == 8 * 256            # the grid cap: 2 KiB at most
+    assert q(FAKE, (1 << 40)) == 8 * 256
+
+
+def test_gemm_workspace_size(lib):
+    f16 = lib.operatorlib_gemm_f16_workspace_size
+    f32 = lib.operatorlib_gemm_f32_workspace_size
+    # decode: 32 column blocks x 16 K splits of 256 rows, fp32 partials
+    assert f16(FAKE, FAKE, 1, 4096, 4096) == 16 * 1 * 4096 * 4
+    # 4095^3 fp16: A padded to [4095, 4096], B to [4096, 4096]
+    assert f16(FAKE, FAKE, 4095, 4095, 4095) == (4095 * 4096 * 2 + 255) // 256 * 256 + 4096 * 4096 * 2
+    # fp32 reads unaligned rows directly: never padded
+    assert f32(FAKE, FAKE, 4095, 4095, 4095) == 0
+    assert f32(FAKE, FAKE, 4096, 4096, 4096) == 0
+    assert f16(NULL, FAKE, 4095, 4095, 4095) == 0  # invalid arguments
+
+
+@pytest.mark.parametrize("bytes_given", [0, 1000])
+def test_gemm_ws_rejects_short_workspace(lib, bytes_given):
+    ws = ctypes.c_void_p(0x100000) if bytes_given else NULL
+    assert lib.operatorlib_gemm_f16_ws(FAKE, FAKE, FAKE, 4095, 4095, 4095, ws, bytes_given,
+                                       NULL) == INVALID
+    assert lib.operatorlib_gemm_f16_ws(FAKE, FAKE, FAKE, 1, 4096, 4096, ws, bytes_given,
+                                       NULL) == INVALID
+
+
+def test_ws_rejects_misaligned_workspace(lib):
+    need = lib.operatorlib_reduce_sum_f32_workspace_size(FAKE, 1 << 24)
+    ws = ctypes.c_void_p(0x100000 + 16)  # 16-byte, not 256-byte, aligned
+    assert lib.operatorlib_reduce_sum_f32_ws(FAKE, FAKE, 1 << 24, ws, need + 256,
+                                             NULL) == INVALID
+
+
+def test_attention_workspace_size(lib):
+    q = lib.operatorlib_attention_f32_workspace_size
+    # B1 H4 S256 D128: 8 query blocks of 128 rows; 4 key splits (256 / 8
+    # workgroups capped at 4, S / 64-key tiles allows 4) of [rows][D + 2]
+    assert q(FAKE, FAKE, FAKE, FAKE, 1, 4, 256, 128, 0) == 4 * 4 * 256 * 130 * 4
+    assert q(FAKE, FAKE, FAKE, FAKE, 1, 4, 256, 129, 0) == 0  # invalid: D > 128
+    h = lib.operatorlib_attention_f16_workspace_size
+    assert h(FAKE, FAKE, FAKE, FAKE, 4, 32, 8192, 128, 1) == 0  # fast path: none

@@ -4,11 +4,12 @@
   capturing stream, is recorded into one graph; the graph is replayed
   several times with eager work and synchronizations between replays, and
   every replay must reproduce the eager results bit for bit (the launchers
-  allocate nothing after their first call on a stream and record no memset
-  nodes).
+  allocate nothing and record no memset nodes; the binding's workspaces
+  come from torch's allocator, which under capture serves the graph's own
+  pool).
 * Concurrency: two host threads launch on two streams at once; both get the
-  results a single thread gets (the launchers are reentrant, and library
-  scratch is per stream).
+  results a single thread gets (the launchers are reentrant, and the
+  binding gives every call a workspace of its own on its stream).
 """
 
 from __future__ import annotations
@@ -70,7 +71,7 @@ def test_graph_capture_replays_match_eager(ops, device):
     t = _inputs(device)
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
-        eager = [y.clone() for y in _all_ops(ops, t)]  # also first use of scratch
+        eager = [y.clone() for y in _all_ops(ops, t)]
     stream.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
