@@ -552,8 +552,21 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
 
     if want("gemm") or want("vendor"):
         # Not operatorlib: the vendor library on the same shapes, timed the
-        # same way (torch.mm on fp16 with an fp32 result -> hipBLASLt, fp32
-        # accumulation and fp32 C, as operatorlib computes them).
+        # same way. fp32: torch.mm on fp32 (the reference's SGEMM comparator
+        # is cuBLAS, README.md:30).
+        gen = torch.Generator(device=dev).manual_seed(26)
+        da = torch.rand((4096, 4096), device=dev, generator=gen) * 2 - 1
+        db = torch.rand((4096, 4096), device=dev, generator=gen) * 2 - 1
+        prev = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = False  # true fp32, as gemm_f32
+        f = lambda i: torch.mm(da, db)
+        out.append(fl_entry("vendor: torch.mm fp32 (hipBLASLt)", [4096, 4096, 4096],
+                            2 * 4096 ** 3, time_launches(torch, f, max(5, min(steps, 20)), 3),
+                            FP32_PEAK_TFLOPS))
+        torch.backends.cuda.matmul.allow_tf32 = prev
+        del da, db
+        # fp16: torch.mm with an fp32 result -> hipBLASLt, fp32 accumulation
+        # and fp32 C, as operatorlib computes them.
         for size in (8192, 4096, 4095):
             gen = torch.Generator(device=dev).manual_seed(26)
             da = (torch.rand((size, size), device=dev, generator=gen) * 2 - 1).half()
@@ -589,7 +602,10 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         out.append(e)
         del bs, a, c
 
-    attn_cases = [(1, 12, 1024, False), (1, 12, 1024, True), (4, 32, 8192, True)]
+    # BASELINE configs, then the reference's one long-sequence published
+    # point (B1 H8 S4096 D128 non-causal, attention/reports/v7.md:112-113).
+    attn_cases = [(1, 12, 1024, False), (1, 12, 1024, True), (4, 32, 8192, True),
+                  (1, 8, 4096, False)]
     for bsz, heads, seq, causal in attn_cases:
         if not want("attention"):
             break
@@ -606,6 +622,8 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         t = time_launches(torch, f, reps, 3)
         extra = {"dense_convention_TFLOPs": round(dense / (t["ms_mean"] * 1e-3) / 1e12, 2),
                  "causal": causal, "flops_convention": "effective (unmasked)"}
+        if (bsz, heads, seq, causal) == (1, 8, 4096, False):
+            extra["reference_orin_ms"] = 223.6
         out.append(fl_entry("attention_f16", list(shape), eff, t, FP16_PEAK_TFLOPS, extra))
         if (bsz, heads, seq) == (4, 32, 8192) and (want("attention") or want("vendor")):
             # Not operatorlib: PyTorch's fused SDPA on the same inputs, timed
@@ -641,6 +659,27 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
                             {"causal": causal}))
         del qkv, o
     torch.cuda.empty_cache()
+    return out
+
+
+def summarize_ops(ops):
+    """{"<op> <shape>": [us, rate, frac]} for every timed op entry."""
+    short = {"stream_copy (calibration, ": "copy ", "stream_read (calibration, 64 MiB read-only)":
+             "read 64MiB", "device_copy (torch, 64 MiB each way)": "torch copy 64MiB",
+             "vendor: ": "", " MiB each way)": "MiB", "(hipBLASLt)": "blaslt",
+             "fp16 -> fp32 C ": "", "(fused, fp16 O)": "", " skinny": ""}
+    out = {}
+    for o in ops:
+        if not o.get("ms") or "shape" not in o:
+            continue
+        name = o["op"]
+        for k, v in short.items():
+            name = name.replace(k, v)
+        key = f"{name} {'x'.join(str(d) for d in o['shape'])}"
+        if "causal" in o and o["causal"]:
+            key += " causal"
+        rate = o.get("GBps", o.get("TFLOPs"))
+        out[key.replace("  ", " ")] = [round(o["ms"] * 1000, 2), rate, o.get("roofline_frac")]
     return out
 
 
@@ -932,8 +971,12 @@ def main():
         "cpu_torch_ops": torch_ops,
         "ops": ops,
         "device": torch.cuda.get_device_name(0),
+        # Last, so that a reader of the output's tail sees every op: per op
+        # and shape, [microseconds per launch, GB/s or TFLOP/s, fraction of
+        # the roofline].
+        "summary": summarize_ops(ops),
     }
-    print(json.dumps(line))
+    print(json.dumps(line, separators=(",", ":")))
 
 
 if __name__ == "__main__":

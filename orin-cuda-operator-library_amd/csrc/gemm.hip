@@ -1308,7 +1308,7 @@ Plan plan(int m, int n, int k, std::size_t capacity) {
 // Runs plan `p` (p.ok); `partials` holds p.bytes of scratch when p.splits > 1.
 template <typename T>
 hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k, const Plan& p,
-                  void* partials, hipStream_t stream) {
+                  void* partials, opl::ScratchLease* lease, hipStream_t stream) {
   using C = Cfg<T>;
   const int blocks_n = (n + C::kBlockN - 1) / C::kBlockN;
   float* dst = p.splits > 1 ? static_cast<float*>(partials) : c;
@@ -1328,10 +1328,14 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k, const P
   else if (m <= 8) launch_m<T, 8>(a, b, dst, m, n, k, chunk, grid, stream);
   else launch_m<T, 16>(a, b, dst, m, n, k, chunk, grid, stream);
   if (p.splits > 1) {
+    const hipError_t status = hipGetLastError();
+    if (status != hipSuccess) return status;
     const long long count = static_cast<long long>(m) * n;
     const long long blocks = (count + kSumThreads - 1) / kSumThreads;
-    sum_splits_kernel<<<dim3(static_cast<unsigned>(blocks < 16384 ? blocks : 16384)),
-                        dim3(kSumThreads), 0, stream>>>(dst, c, count, p.splits);
+    return lease->launch_last(sum_splits_kernel,
+                              dim3(static_cast<unsigned>(blocks < 16384 ? blocks : 16384)),
+                              dim3(kSumThreads), static_cast<const float*>(dst), c, count,
+                              p.splits);
   }
   return hipGetLastError();
 }
@@ -1670,10 +1674,11 @@ GemmPlan plan_gemm(const T* a, const T* b, int m, int n, int k, std::size_t capa
 // Runs plan `p`; `scratch` holds p.bytes (unused when 0).
 template <typename T>
 hipError_t run_gemm(const GemmPlan& p, const T* a, const T* b, float* c, int m, int n, int k,
-                    void* scratch, hipStream_t stream) {
+                    opl::ScratchLease* lease, hipStream_t stream) {
+  void* const scratch = lease != nullptr ? lease->data() : nullptr;
   switch (p.kind) {
     case GemmPlan::kSkinny:
-      return skinny::launch<T>(a, b, c, m, n, k, p.skinny, scratch, stream);
+      return skinny::launch<T>(a, b, c, m, n, k, p.skinny, scratch, lease, stream);
     case GemmPlan::kDma:
     case GemmPlan::kPaddedDma:
       if constexpr (std::is_same<T, _Float16>::value) {
@@ -1705,7 +1710,7 @@ int gemm_entry(const T* a, const T* b, float* c, int m, int n, int k,
   // Held until the last kernel that reads the scratch is enqueued.
   opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
   if (lease.status() != hipSuccess) return lease.status();
-  return run_gemm<T>(p, a, b, c, m, n, k, lease.data(), stream);
+  return run_gemm<T>(p, a, b, c, m, n, k, &lease, stream);
 }
 
 const _Float16* as_f16(const operatorlib_half_t* p) {

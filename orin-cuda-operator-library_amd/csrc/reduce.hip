@@ -205,7 +205,13 @@ int reduce_with(const float* input, float* output, std::size_t n,
   // Held until the combine kernel is enqueued (scratch.hpp).
   opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
   if (lease.status() != hipSuccess) return lease.status();
-  return enqueue(input, output, n, p, static_cast<double*>(lease.data()), stream);
+  double* partials = static_cast<double*>(lease.data());
+  reduce_partials_kernel<<<p.blocks, kThreads, 0, stream>>>(input, output, n, p.head, p.nvec,
+                                                            partials);
+  const hipError_t status = hipGetLastError();
+  if (status != hipSuccess) return status;
+  return lease.launch_last(reduce_combine_kernel, dim3(1), dim3(kCombineThreads),
+                           static_cast<const double*>(partials), p.blocks, output);
 }
 
 }  // namespace

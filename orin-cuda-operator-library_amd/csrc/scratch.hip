@@ -62,8 +62,11 @@ hipError_t current_device(ScratchLease::Device** out) {
     }
     void* base = nullptr;
     status = hipGetSymbolAddress(&base, HIP_SYMBOL(arena));
+    // A device-scope release is all that ordering arena users on one GPU
+    // needs.
     if (status == hipSuccess)
-      status = hipEventCreateWithFlags(&fresh->done, hipEventDisableTiming);
+      status = hipEventCreateWithFlags(&fresh->done,
+                                       hipEventDisableTiming | hipEventReleaseToDevice);
     hipStreamCaptureMode restore = mode;
     const hipError_t restored = hipThreadExchangeStreamCaptureMode(&restore);
     if (status == hipSuccess) status = restored;
@@ -118,12 +121,17 @@ ScratchLease::ScratchLease(hipStream_t stream, void* workspace, std::size_t byte
   capacity_ = kArenaBytes;
 }
 
+hipEvent_t ScratchLease::chain_event() const {
+  return device_ != nullptr && !capturing_ ? device_->done : nullptr;
+}
+
 ScratchLease::~ScratchLease() {
   if (device_ == nullptr) return;
-  // The event is recorded even after a failed launch: the stream already
-  // waits for the previous sequence, so the record still marks a point
-  // after every earlier arena sequence, which is all a later waiter needs.
-  if (!capturing_ && hipEventRecord(device_->done, stream_) == hipSuccess) {
+  // Unless the last launch carried it, the event is recorded here, even
+  // after a failed launch: the stream already waits for the previous
+  // sequence, so the record still marks a point after every earlier arena
+  // sequence, which is all a later waiter needs.
+  if (!capturing_ && (recorded_ || hipEventRecord(device_->done, stream_) == hipSuccess)) {
     device_->last = stream_;
     device_->recorded = true;
   }

@@ -346,6 +346,43 @@ def test_gemm_skinny_unaligned_a(hip, m, dtype):
         assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
 
 
+# M <= 16 at wide N (the LLM decode range): ragged K (a partial last split,
+# K below one k block), N off a multiple of the column block, element-wise
+# A loads (offset 1), M 1-16; results deterministic.
+GEMM_DECODE = [(1, 4104, 1000), (7, 3080, 33), (16, 4096, 4095), (2, 4096, 17),
+               (16, 6144, 1024), (1, 3072, 1), (11, 12288, 512), (3, 4112, 4100)]
+
+
+@pytest.mark.parametrize("mnk", GEMM_DECODE)
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_gemm_skinny_wide(hip, mnk, offset, dtype):
+    m, n, k = mnk
+    a = oracle.uniform(670 + m, (m, k))
+    b = oracle.uniform(671 + n, (k, n))
+    if dtype == "f16":
+        ab, bb = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        fn, ref = hip.lib.operatorlib_gemm_f16, oracle.gemm(oracle.from_f16_bits(ab),
+                                                             oracle.from_f16_bits(bb))
+        a, b = ab, bb
+    else:
+        fn, ref = hip.lib.operatorlib_gemm_f32, oracle.gemm(a, b)
+    da, db = to_device(a, offset), to_device(b)  # A may be misaligned, B is not
+    out = empty((m, n))
+    check(fn(ptr(da), ptr(db), ptr(out), m, n, k, stream_handle()), "gemm")
+    torch.cuda.synchronize()
+    y = out.cpu().numpy().astype(np.float64)
+    if dtype == "f16":
+        assert np.max(np.abs(y - ref)) <= 2e-3
+    else:
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
+        assert np.all(np.abs(y - ref) <= 1e-3 + 1e-3 * np.abs(ref))
+    # deterministic
+    check(fn(ptr(da), ptr(db), ptr(out), m, n, k, stream_handle()), "gemm")
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().astype(np.float64), y)
+
+
 def test_gemm_skinny_deterministic(hip):
     a = oracle.uniform(650, (8, 4096))
     b = oracle.uniform(651, (4096, 2048))

@@ -63,11 +63,12 @@ def test_reduce_ws_matches_plain(lib, n):
     assert abs(y.item() - ref) <= 1e-5 * abs(ref)
 
 
-# (m, n, k, dtype): decode shapes on both skinny kernels, padded 1000^3 and
+# (m, n, k, dtype): narrow decode shapes (split K) on both skinny kernels,
+# padded 1000^3 and
 # 4095^3 fp16, a 272-tile fp16 grid whose last round is split, an aligned
 # shape that needs no scratch.
-GEMM_CASES = [(1, 4096, 4096, "f16"), (16, 4096, 4096, "f16"), (1, 4096, 4096, "f32"),
-              (16, 4096, 4096, "f32"), (1000, 1000, 1000, "f16"), (4095, 4095, 4095, "f16"),
+GEMM_CASES = [(1, 1024, 4096, "f16"), (16, 1024, 4096, "f16"), (1, 1024, 4096, "f32"),
+              (16, 1024, 4096, "f32"), (1000, 1000, 1000, "f16"), (4095, 4095, 4095, "f16"),
               (4352, 4096, 512, "f16"), (1024, 1024, 1024, "f16"), (999, 1001, 1003, "f32")]
 
 

@@ -207,8 +207,11 @@ def test_reduce_workspace_size(lib):
 def test_gemm_workspace_size(lib):
     f16 = lib.operatorlib_gemm_f16_workspace_size
     f32 = lib.operatorlib_gemm_f32_workspace_size
-    # decode: 32 column blocks x 16 K splits of 256 rows, fp32 partials
+    # decode: 32 column blocks of 128 x 16 K splits of 256 rows, fp32 partials
     assert f16(FAKE, FAKE, 1, 4096, 4096) == 16 * 1 * 4096 * 4
+    assert f32(FAKE, FAKE, 16, 4096, 4096) == 8 * 16 * 4096 * 4  # 64 blocks of 64 x 8
+    # 8 column blocks x 64 K splits of 64 rows
+    assert f16(FAKE, FAKE, 1, 1024, 4096) == 64 * 1 * 1024 * 4
     # 4095^3 fp16: A padded to [4095, 4096], B to [4096, 4096]
     assert f16(FAKE, FAKE, 4095, 4095, 4095) == (4095 * 4096 * 2 + 255) // 256 * 256 + 4096 * 4096 * 2
     # fp32 reads unaligned rows directly: never padded
@@ -222,7 +225,7 @@ def test_gemm_ws_rejects_short_workspace(lib, bytes_given):
     ws = ctypes.c_void_p(0x100000) if bytes_given else NULL
     assert lib.operatorlib_gemm_f16_ws(FAKE, FAKE, FAKE, 4095, 4095, 4095, ws, bytes_given,
                                        NULL) == INVALID
-    assert lib.operatorlib_gemm_f16_ws(FAKE, FAKE, FAKE, 1, 4096, 4096, ws, bytes_given,
+    assert lib.operatorlib_gemm_f16_ws(FAKE, FAKE, FAKE, 1, 1024, 4096, ws, bytes_given,
                                        NULL) == INVALID
 
 

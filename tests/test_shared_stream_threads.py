@@ -5,7 +5,7 @@ through the C ABI (ctypes releases the GIL, so both threads are inside the
 library together):
   * reduce_sum_f32 over 1,000,003 values (one fp64 partial per workgroup,
     then the combine kernel);
-  * gemm_f16 1 x 4096 x 4096 (decode GEMM, split-K partials + split sum);
+  * gemm_f16 1 x 1024 x 4096 (decode GEMM, split-K partials + split sum);
   * gemm_f16 1000^3 (K and N not multiples of the fast kernel's steps:
     zero-padded operand copies, then the product);
   * attention_f32 B1 H4 S256 D128 (small grid: keys split over workgroups,
@@ -47,6 +47,7 @@ from gpu_util import check, ptr, to_device
 pytestmark = pytest.mark.gpu
 
 ROUNDS = 50
+SKINNY_N = 1024  # decode GEMM width: 8 column blocks x 64 K splits
 HIP_STREAM_PER_THREAD = 2  # hipStreamPerThread, include/hip/hip_runtime_api.h
 # Split-tail GEMM: [M, K] x [K, N]; rows checked against the oracle: two in
 # every 256-row tile row, its first and last.
@@ -62,7 +63,7 @@ class Case:
     def __init__(self, seed: int, rounds: int):
         self.x = oracle.uniform(seed, 1_000_003)
         self.a1 = oracle.to_f16_bits(oracle.uniform(seed + 1, (1, 4096)))
-        self.b1 = oracle.to_f16_bits(oracle.uniform(seed + 2, (4096, 4096)))
+        self.b1 = oracle.to_f16_bits(oracle.uniform(seed + 2, (4096, SKINNY_N)))
         self.ap = oracle.to_f16_bits(oracle.uniform(seed + 3, (1000, 1000)))
         self.bp = oracle.to_f16_bits(oracle.uniform(seed + 4, (1000, 1000)))
         self.q, self.k, self.v = (oracle.normal(seed + 5 + i, (1, 4, 256, 128)) for i in range(3))
@@ -80,7 +81,7 @@ class Case:
                     for name in ("x", "a1", "b1", "ap", "bp", "q", "k", "v", "at", "bt")}
         self.out = {
             "reduce": torch.full((rounds,), float("nan"), device="cuda"),
-            "skinny": torch.full((rounds, 1, 4096), float("nan"), device="cuda"),
+            "skinny": torch.full((rounds, 1, SKINNY_N), float("nan"), device="cuda"),
             "padded": torch.full((rounds, 1000, 1000), float("nan"), device="cuda"),
             "attn": torch.full((rounds, 1, 4, 256, 128), float("nan"), device="cuda"),
             "tail": torch.full((rounds, TAIL_MK[0], TAIL_N), float("nan"), device="cuda"),
@@ -91,7 +92,7 @@ class Case:
         check(lib.operatorlib_reduce_sum_f32(ptr(d["x"]), ptr(o["reduce"][r:]), d["x"].numel(),
                                              stream), "reduce")
         check(lib.operatorlib_gemm_f16(ptr(d["a1"]), ptr(d["b1"]), ptr(o["skinny"][r]),
-                                       1, 4096, 4096, stream), "gemm_f16 skinny")
+                                       1, SKINNY_N, 4096, stream), "gemm_f16 skinny")
         check(lib.operatorlib_gemm_f16(ptr(d["ap"]), ptr(d["bp"]), ptr(o["padded"][r]),
                                        1000, 1000, 1000, stream), "gemm_f16 padded")
         check(lib.operatorlib_attention_f32(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),
@@ -107,7 +108,8 @@ class Case:
         tmp = torch.empty(TAIL_MK[0] * TAIL_N, device="cuda")
         return max(
             lib.operatorlib_reduce_sum_f32_workspace_size(ptr(d["x"]), d["x"].numel()),
-            lib.operatorlib_gemm_f16_workspace_size(ptr(d["a1"]), ptr(d["b1"]), 1, 4096, 4096),
+            lib.operatorlib_gemm_f16_workspace_size(ptr(d["a1"]), ptr(d["b1"]), 1, SKINNY_N,
+                                                    4096),
             lib.operatorlib_gemm_f16_workspace_size(ptr(d["ap"]), ptr(d["bp"]), 1000, 1000,
                                                     1000),
             lib.operatorlib_attention_f32_workspace_size(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),
@@ -123,7 +125,7 @@ class Case:
         check(lib.operatorlib_reduce_sum_f32_ws(ptr(d["x"]), ptr(o["reduce"][r:]),
                                                 d["x"].numel(), w, nb, stream), "reduce_ws")
         check(lib.operatorlib_gemm_f16_ws(ptr(d["a1"]), ptr(d["b1"]), ptr(o["skinny"][r]),
-                                          1, 4096, 4096, w, nb, stream), "gemm_f16_ws skinny")
+                                          1, SKINNY_N, 4096, w, nb, stream), "gemm_f16_ws skinny")
         check(lib.operatorlib_gemm_f16_ws(ptr(d["ap"]), ptr(d["bp"]), ptr(o["padded"][r]),
                                           1000, 1000, 1000, w, nb, stream), "gemm_f16_ws padded")
         check(lib.operatorlib_attention_f32_ws(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),

@@ -59,6 +59,8 @@ def _all_ops(ops, t):
         ops.gemm(t["ah"], t["bh"]),      # zero-padded workspace path
         ops.gemm(t["a1"], t["b1"]),      # skinny path with K splits
         ops.gemm(t["a16"], t["b1"]),     # matrix-core skinny kernel, vector A
+        ops.gemm(t["a1"], t["b1"][:, :1024].contiguous()),   # narrow: more K splits
+        ops.gemm(t["a16"], t["b1"][:, :1024].contiguous()),
         ops.gemm(t["a12"], t["b32"]),    # same, fp32
         ops.attention(t["q"], t["k"], t["v"], True),
         # fp32, 8 query blocks: keys split over workgroups, partials in the
