@@ -62,11 +62,15 @@ hipError_t current_device(ScratchLease::Device** out) {
     }
     void* base = nullptr;
     status = hipGetSymbolAddress(&base, HIP_SYMBOL(arena));
-    // A device-scope release is all that ordering arena users on one GPU
-    // needs.
+    // Arena users all run on this GPU, so the event needs no system-scope
+    // fence: each kernel's own end-of-kernel (device-scope) release already
+    // makes its writes visible to later kernels on the GPU, whatever their
+    // stream. With the default system-scope fence every record flushed the
+    // caches for the host: ~1.2 us per call as a stop event, ~2.8 us as a
+    // separate record, against ~0.2 / ~0.7 us without it (13 us reduce).
     if (status == hipSuccess)
       status = hipEventCreateWithFlags(&fresh->done,
-                                       hipEventDisableTiming | hipEventReleaseToDevice);
+                                       hipEventDisableTiming | hipEventDisableSystemFence);
     hipStreamCaptureMode restore = mode;
     const hipError_t restored = hipThreadExchangeStreamCaptureMode(&restore);
     if (status == hipSuccess) status = restored;

@@ -28,7 +28,8 @@
 //       - holds that GPU's host mutex while the sequence is enqueued,
 //       - makes the stream wait (hipStreamWaitEvent) for the end of the
 //         previous arena sequence when that one ran on another stream,
-//       - records the end of its own sequence in the GPU's event.
+//       - records the end of its own sequence in the GPU's event (with no
+//         system-scope fence: only this GPU's kernels wait on it).
 //     Arena sequences therefore run one after another on the device,
 //     whatever streams and host threads issue them, and nothing blocks the
 //     host. Library-held device memory is kArenaBytes per GPU (plus the
@@ -74,8 +75,8 @@ class ScratchLease {
   // Enqueues `kernel` as the sequence's last launch. On the eager arena the
   // chain's event rides on it as hipExtLaunchKernel's stop event, so it
   // completes with the kernel: a separate hipEventRecord at release adds a
-  // marker of its own, measured at ~2.8 us per call on a 13 us reduce (the
-  // stop event: ~1.2 us). Elsewhere (a caller workspace, capture) it is a
+  // marker of its own, measured at ~0.7 us per call on a 13 us reduce (the
+  // stop event: ~0.2 us). Elsewhere (a caller workspace, capture) it is a
   // plain launch. Sequences whose last launch is a long kernel leave the
   // record to the destructor instead.
   template <typename... Params, typename... Args>

@@ -87,6 +87,42 @@ def test_reduce_two_streams(lib):
         assert abs(o.item() - ref) <= 1e-5 * abs(ref)
 
 
+def test_arena_orders_four_streams(lib):
+    """Reduce and split-K decode GEMM calls interleaved over four streams all
+    use the GPU's arena; its event chain must order every sequence after the
+    previous one, so every output matches the oracle (a missed wait would let
+    one call's partials overwrite another's)."""
+    from gpu_util import ptr, stream_handle, to_device
+    streams = [torch.cuda.Stream() for _ in range(4)]
+    xs = [oracle.uniform(90 + i, 1_000_003 + 17 * i) for i in range(4)]
+    dx = [to_device(x) for x in xs]
+    a = [oracle.to_f16_bits(oracle.uniform(95 + i, (16, 2048))) for i in range(4)]
+    b = [oracle.to_f16_bits(oracle.uniform(99 + i, (2048, 1024))) for i in range(4)]
+    da, db = [to_device(t) for t in a], [to_device(t) for t in b]
+    rounds = 25
+    red = torch.full((rounds, 4), float("nan"), device="cuda")
+    gem = torch.full((rounds, 4, 16, 1024), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    for r in range(rounds):
+        for i, st in enumerate(streams):
+            h = stream_handle(st)
+            assert lib.operatorlib_reduce_sum_f32(ptr(dx[i]), ptr(red[r, i:]), dx[i].numel(),
+                                                  h) == 0
+            assert lib.operatorlib_gemm_f16(ptr(da[i]), ptr(db[i]), ptr(gem[r, i]), 16, 1024,
+                                            2048, h) == 0
+    torch.cuda.synchronize()
+    red_h = red.cpu().numpy()
+    gem_h = gem.cpu().numpy().astype(np.float64)
+    for i in range(4):
+        ref = oracle.reduce_sum(xs[i])
+        gref = oracle.gemm(oracle.from_f16_bits(a[i]), oracle.from_f16_bits(b[i]))
+        for r in range(rounds):
+            assert abs(red_h[r, i] - ref) <= 1e-5 * abs(ref), (r, i)
+            assert red_h[r, i] == red_h[0, i], (r, i)
+            assert np.max(np.abs(gem_h[r, i] - gref)) <= 2e-3, (r, i)
+            assert np.array_equal(gem_h[r, i], gem_h[0, i]), (r, i)
+
+
 # ----------------------------------------------------------------------- softmax
 
 SOFTMAX_SHAPES = [(19, 128), (17, 1024), (17, 1003), (5, 1), (3, 7), (1, 4096),
