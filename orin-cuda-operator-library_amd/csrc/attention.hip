@@ -41,7 +41,7 @@
 //   * grids too small to fill the GPU split each query block's keys: the
 //     fp16 fast path between two or four wavefront groups of one workgroup
 //     (merged through LDS), the register-staged kernel over several workgroups
-//     (partials in the stream's workspace, merged by
+//     (partials in scratch, the GPU's arena or the caller's workspace, merged by
 //     attention_combine_kernel in split order).
 // Head dims are padded to a multiple of 32 with zeros (any 1 <= D <= 128).
 
@@ -51,7 +51,6 @@
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
-#include <optional>
 #include <type_traits>
 
 #include "common.hpp"

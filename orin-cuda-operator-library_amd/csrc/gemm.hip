@@ -12,12 +12,13 @@
 //     operands): direct global->LDS loads, described before the kernel;
 //     256 x 256 tiles, or 128 x 128 when the grid would leave CUs idle;
 //   * large shapes that miss those rules (e.g. 4095^3): zero-padded copies
-//     of the operands in the stream's workspace, then the fast kernels;
-//   * gemm_mfma_kernel "vector" instance: 16-byte register-staged chunks,
-//     16-byte aligned rows (all fp32 shapes with K, N % 4 == 0); fp32 uses
-//     128 x 128 tiles on small grids;
-//   * gemm_mfma_kernel "general" instance: element-wise staging with zero
-//     fill, any shape and alignment.
+//     of the operands in scratch (the GPU's arena or the caller's workspace),
+//     then the fast kernels (fp16; fp32 reads unaligned rows directly);
+//   * gemm_mfma_kernel, register-staged (Staging below): 16-byte chunks from
+//     16-byte aligned rows (K, N multiples of the chunk, aligned operands),
+//     or 16-byte chunks at 4-byte alignment (every fp32 shape; fp16 with even
+//     K and N), or element-wise with zero fill (any shape and alignment);
+//     fp32 uses 128 x 128 tiles on small grids.
 // Every path but the vector-ALU skinny kernel (M <= 4 fp16, M <= 8 fp32)
 // runs on the matrix cores.
 //
@@ -46,9 +47,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
-#include <optional>
 #include <type_traits>
 
 #include "common.hpp"
@@ -847,7 +848,7 @@ __global__ __launch_bounds__(256) void sum_tail_kernel(float* __restrict__ C, in
 //     column (lane shuffles), then across the 4 wavefronts through LDS, in
 //     a fixed order;
 //   * K is split over enough workgroups to fill the GPU; per-split partials
-//     go to the stream's workspace and a second kernel sums them in split
+//     go to scratch (arena or workspace) and a second kernel sums them in split
 //     order, so results are deterministic;
 //   * from M = 5 (fp16) or 9 (fp32) the vector-ALU dot products cost more
 //     than the B stream, and skinny_mfma_kernel (below) takes over.
@@ -1558,11 +1559,20 @@ hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
 constexpr int kTailMaxSplits = 16;
 constexpr int kTailMinDepth = 256;
 
+// CUs of the current device, looked up once per device (0 if unknown).
 int device_cus() {
-  int device = 0, cus = 0;
-  if (hipGetDevice(&device) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> known[kMaxDevices] = {};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 0;
+  if (device >= 0 && device < kMaxDevices) {
+    const int cached = known[device].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return 0;
+  if (device >= 0 && device < kMaxDevices) known[device].store(cus, std::memory_order_relaxed);
   return cus;
 }
 
