@@ -706,6 +706,12 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
     // landed (sync_stage), so substep 1 refills `cur` with step + 2 and
     // reads the next step's first fragments from `nxt` under its MFMAs: the
     // barrier never waits on an LDS read.
+    // The second substep (copies, next fragments, MFMAs) runs at raised
+    // wave priority: the waves that left the barrier first get their
+    // copies and reads issued ahead of the SIMD's other wavefront. Measured
+    // on MI355X (us, 8192^3 / 4096^3, two runs each): 883.0, 884.1 ->
+    // 873.2, 869.8 / 107.1, 106.0 -> 105.2, 105.1; raising it for the first
+    // substep instead was slower (896.1).
     auto tile = [&](unsigned char* cur, unsigned char* nxt, int step) {
       load(cur, 1, f1);
       mma(f0);
@@ -713,11 +719,13 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
       __builtin_amdgcn_sched_barrier(0);
       sync_stage();
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
       issue(cur, step + 2);
       load(nxt, 0, f0);
       mma(f1);
       interleave(true);
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(0);
     };
     issue(stage0, 0);
     issue(stage1, 1);
