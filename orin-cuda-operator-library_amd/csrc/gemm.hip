@@ -1,19 +1,22 @@
 // Row-major GEMM C[M,N] = A[M,K] * B[K,N] on the CDNA4 matrix cores.
 //   gemm_f16: fp16 A/B, v_mfma_f32_16x16x32_f16 (direct-to-LDS kernel) or
 //             v_mfma_f32_32x32x16_f16 (register-staged), fp32 accumulate and output
-//   gemm_f32: fp32 A/B, v_mfma_f32_32x32x2_f32,  fp32 accumulate and output
+//   gemm_f32: fp32 A/B, v_mfma_f32_16x16x4_f32 (direct-to-LDS kernel) or
+//             v_mfma_f32_32x32x2_f32 (register-staged), fp32 accumulate and output
 //
 // Reference: operatorlib::gemm_f16 / gemm_f32 (src/gemm.cu:440-479). The
 // reference dispatches between WMMA, cp.async register-tiled and scalar
 // kernels on divisibility; here the dispatch is, in order:
 //   * M <= 16 (decode shapes): the skinny kernels (namespace skinny), an
 //     HBM stream over B with split K and an ordered split sum;
-//   * gemm_f16_dma_kernel (fp16, K % 32 == 0, N % 8 == 0, 16-byte aligned
-//     operands): direct global->LDS loads, described before the kernel;
-//     256 x 256 tiles, or 128 x 128 when the grid would leave CUs idle;
-//   * large shapes that miss those rules (e.g. 4095^3): zero-padded copies
-//     of the operands in scratch (the GPU's arena or the caller's workspace),
-//     then the fast kernels (fp16; fp32 reads unaligned rows directly);
+//   * gemm_dma_kernel (fp16: K % 32 == 0, N % 8 == 0; fp32: K % 16 == 0,
+//     N % 4 == 0; 16-byte aligned operands): direct global->LDS loads,
+//     described before the kernel; 256 x 256 tiles, or 128 x 128 when the
+//     grid would leave CUs idle;
+//   * large fp16 shapes that miss those rules (e.g. 4095^3): zero-padded
+//     copies of the operands in scratch (the GPU's arena or the caller's
+//     workspace), then the direct-to-LDS kernel (fp32 ones read their rows
+//     in place, below);
 //   * gemm_mfma_kernel, register-staged (Staging below): 16-byte chunks from
 //     16-byte aligned rows (K, N multiples of the chunk, aligned operands),
 //     or 16-byte chunks at 4-byte alignment (every fp32 shape; fp16 with even
@@ -384,8 +387,9 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 }
 
 // ---------------------------------------------------------------------------
-// gemm_f16_dma_kernel — the fp16 fast path (K % 32 == 0, N % 8 == 0, 16-byte
-// aligned A and B).
+// gemm_dma_kernel — the fast path of both precisions (16-byte aligned A
+// and B; fp16: K % 32 == 0, N % 8 == 0; fp32: K % 16 == 0, N % 4 == 0).
+// Described for fp16; fp32 differences at the end.
 //
 //   * 256 x 256 C tile per 512-thread workgroup: 8 wavefronts as 2 (M) x 4
 //     (N), each owning 128 x 64 = 8 x 4 MFMA 16x16x32 blocks (128 fp32
@@ -435,6 +439,21 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 // 852-871 us (1.26-1.29 PFLOP/s); hipBLASLt with the same fp32 C: 112-116
 // and 827-859 us. With v_mfma_f32_32x32x16_f16 the same schedule ran
 // 111-119 / 890-910 us, bit-identical output.
+//
+// fp32: the same tiles, stages and schedule with the same A row bytes per
+// step (32 or 16 elements), on v_mfma_f32_16x16x4_f32. A fragments are the
+// same 16-byte chunks; B rows (1 KiB for 256-wide tiles) are read with one
+// ds_read_b32 per lane and MFMA (lane group q reads row 4q + e of the
+// substep, e = 0..3, and A's chunk q), and swizzled chunk ^ 4 * ((k >> 2) &
+// 3) so the four lane groups of a read hit different banks. A substep is
+// 16 deep, 4 MFMAs per 16 x 16 block, interleaved with the reads and copies
+// in groups of one block's 4 MFMAs. The fp32 MFMA rate does not fall under
+// load (a loop of them alone: 155 TFLOP/s, 0.99 of peak), so what the
+// register-staged kernel lost to its VGPR staging, transposes and LDS
+// writes comes back. Measured on MI355X (us, register-staged -> direct):
+// 4096^3 1017 -> 928 (0.94 of the fp32 peak; hipBLASLt 964-979), 8192 x
+// 8192 x 4096 4050 -> 3697, 2048^3 153.5 -> 124.5, 1000 x 4096 x 4096
+// 301 -> 242, 4352 x 4096 x 1024 (split last round) 515 -> 326.
 // ---------------------------------------------------------------------------
 
 namespace dma {
@@ -455,68 +474,115 @@ struct TailSplit {
 };
 #define OPL_LDS __attribute__((address_space(3)))
 
+// Element types of the direct-to-LDS kernel. A substep is the k range one
+// set of fragments covers: every operand fragment is 16 bytes per lane.
+//   * fp16: one v_mfma_f32_16x16x32_f16 per 16 x 16 block and substep of
+//     32; A and B fragments are 8 k-contiguous halves (B read transposed);
+//   * fp32: four v_mfma_f32_16x16x4_f32 per block and substep of 16. Lane
+//     group q (lanes 16q..16q+15) reads A's 16-byte chunk q of the substep
+//     (k = 4q..4q+3) and, for MFMA e, B's row 4q + e: so MFMA e multiplies
+//     k = 4q + e in every lane group, on both operands.
+template <typename T>
+struct Elem;
+template <>
+struct Elem<_Float16> {
+  using Frag = half8;
+  static constexpr int kSubK = 32;
+  static constexpr int kMfmas = 1;  // MFMAs per 16 x 16 block and substep
+  static constexpr int kBReads = 2;  // LDS reads per B fragment
+};
+template <>
+struct Elem<float> {
+  using Frag = floatx4;
+  static constexpr int kSubK = 16;
+  static constexpr int kMfmas = 4;
+  static constexpr int kBReads = 4;
+};
+
 // C tile configurations. BM x BN per workgroup, WM x WN wavefronts of
-// (BM / WM) x (BN / WN); K steps of BK (32 or 64) in `Stages` LDS stages.
-// A rows in LDS are 2 * BK bytes, B rows 2 * BN bytes (BN / 8 16-byte
-// chunks).
-template <int BM, int BN, int WM, int WN, int BK, int Stages>
+// (BM / WM) x (BN / WN); K steps of BK elements (128 or 64 bytes of an A
+// row) in `Stages` LDS stages. B rows in LDS are BN elements (BN *
+// sizeof(T) / 16 16-byte chunks).
+template <typename T, int BM, int BN, int WM, int WN, int BK, int Stages>
 struct Tile {
+  using Type = T;
+  using Frag = typename Elem<T>::Frag;
   static constexpr int kBM = BM, kBN = BN, kBK = BK;
   static constexpr int kWM = WM, kWN = WN;
   static constexpr int kStages = Stages;
-  static constexpr int kSubsteps = BK / 32;  // MFMA k32 substeps per step
+  static constexpr int kSubsteps = BK / Elem<T>::kSubK;  // fragment sets per step
   static constexpr int kThreads = 64 * WM * WN;
   static constexpr int kFM = BM / WM / 16;
   static constexpr int kFN = BN / WN / 16;
-  static constexpr int kARowBytes = BK * 2;
-  static constexpr int kAChunks = BK / 8;
-  static constexpr int kABytes = BM * BK * 2;
-  static constexpr int kBBytes = BK * BN * 2;
-  static constexpr int kBRowBytes = BN * 2;
-  static constexpr int kBChunks = BN / 8;
+  static constexpr int kChunkElems = 16 / static_cast<int>(sizeof(T));
+  static constexpr int kARowBytes = BK * static_cast<int>(sizeof(T));
+  static constexpr int kAChunks = kARowBytes / 16;
+  static constexpr int kABytes = BM * kARowBytes;
+  static constexpr int kBRowBytes = BN * static_cast<int>(sizeof(T));
+  static constexpr int kBBytes = BK * kBRowBytes;
+  static constexpr int kBChunks = kBRowBytes / 16;
   static constexpr int kStage = kABytes + kBBytes;
   // DMA chunks per thread per operand.
   static constexpr int kCopies = kABytes / 16 / kThreads;
   static_assert(kABytes == kBBytes && kCopies * 16 * kThreads == kABytes,
                 "both operand tiles split evenly into 16-byte copies");
   static_assert(64 % kBChunks == 0, "a wavefront copies whole B rows");
-  static_assert((BK == 64 && Stages == 2) || (BK == 32 && Stages == 4),
-                "two 64-deep or four 32-deep stages");
+  static_assert((kARowBytes == 128 && Stages == 2) || (kARowBytes == 64 && Stages == 4),
+                "two 128-byte or four 64-byte stages of A rows");
   // XOR swizzle of A row m's 16-byte chunks: rows 16 apart share it.
   __device__ static int swizzle_a(int m) {
     return kAChunks == 8 ? (m >> 1) & 7 : (m >> 2) & 3;
   }
+  // XOR swizzle of B row k's 16-byte chunks. fp16 (ds_read_b64_tr_b16 of
+  // rows k & 3 and bit 3 of k): chunk ^ 4 * (k & 3) ^ 2 * (bit 3 of k).
+  // fp32 (ds_read_b32, the 16-lane groups of one read on rows 4 apart):
+  // chunk ^ 4 * ((k >> 2) & 3), so the four groups' 64-byte row segments
+  // fall on four different 64-byte bank ranges.
+  __device__ static int swizzle_b(int k) {
+    if constexpr (sizeof(T) == 2)
+      return 4 * (k & 3) ^ 2 * ((k >> 3) & 1);
+    else
+      return 4 * ((k >> 2) & 3);
+  }
 };
 // 256 x 256: 8 wavefronts of 128 x 64, for grids that fill the GPU.
-using BigTile = Tile<256, 256, 2, 4, 64, 2>;
+using BigTile = Tile<_Float16, 256, 256, 2, 4, 64, 2>;
 // The same for K % 64 == 32.
-using BigTileK32 = Tile<256, 256, 2, 4, 32, 4>;
+using BigTileK32 = Tile<_Float16, 256, 256, 2, 4, 32, 4>;
 // 128 x 128: 4 wavefronts of 64 x 64, four times the workgroups for the
 // same C, for grids that would leave CUs idle with BigTile.
-using SmallTile = Tile<128, 128, 2, 2, 32, 4>;
-constexpr int kBK = 32;  // K granularity of every tile configuration
-
-__device__ __forceinline__ int swizzle_b(int k) { return 4 * (k & 3) ^ 2 * ((k >> 3) & 1); }
+using SmallTile = Tile<_Float16, 128, 128, 2, 2, 32, 4>;
+// fp32: the same geometry with the same A row bytes per step (32 or 16
+// elements).
+using BigTileF32 = Tile<float, 256, 256, 2, 4, 32, 2>;
+using BigTileF32K16 = Tile<float, 256, 256, 2, 4, 16, 4>;
+using SmallTileF32 = Tile<float, 128, 128, 2, 2, 16, 4>;
+// K granularity of every tile configuration of an element type.
+template <typename T>
+constexpr int kBK = sizeof(T) == 2 ? 32 : 16;
 
 template <typename Cfg>
 struct Fragments {
-  half8 a[Cfg::kFM];
-  half8 b[Cfg::kFN];
+  typename Cfg::Frag a[Cfg::kFM];
+  typename Cfg::Frag b[Cfg::kFN];
 };
 
 template <typename Cfg, bool kTail = false>
 __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
-                         const _Float16* __restrict__ B,
-                         float* __restrict__ C, int M, int N, int K, int ldb,
-                         TailSplit tail) {
+void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
+                     const typename Cfg::Type* __restrict__ B,
+                     float* __restrict__ C, int M, int N, int K, int ldb,
+                     TailSplit tail) {
+  using T = typename Cfg::Type;
+  using E = Elem<T>;
   constexpr int kBM = Cfg::kBM, kBN = Cfg::kBN, kBK = Cfg::kBK;
   constexpr int kWM = Cfg::kWM, kWN = Cfg::kWN;
   constexpr int kFM = Cfg::kFM, kFN = Cfg::kFN;
   constexpr int kABytes = Cfg::kABytes, kCopies = Cfg::kCopies;
   constexpr int kBChunks = Cfg::kBChunks;
-  constexpr int kReads = kFM + 2 * kFN;  // LDS read instructions per k32 substep
-  constexpr int kIssues = 2 * kCopies;   // DMA instructions per K step
+  constexpr int kSize = static_cast<int>(sizeof(T));
+  constexpr int kReads = kFM + E::kBReads * kFN;  // LDS read instructions per substep
+  constexpr int kIssues = 2 * kCopies;            // DMA instructions per K step
   static_assert(kWM == 2, "A fragment offsets assume two wavefront rows");
 
   const int tiles_m = (M + kBM - 1) / kBM;
@@ -569,10 +635,10 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
     const int slot = (wave * kCopies + j) * 64 + lane;
     const int m = slot / Cfg::kAChunks;
     const int chunk = (slot % Cfg::kAChunks) ^ Cfg::swizzle_a(m);
-    a_dma[j] = (min(m0 + m, M - 1) - m0) * K * 2 + 16 * chunk;
+    a_dma[j] = (min(m0 + m, M - 1) - m0) * K * kSize + 16 * chunk;
     const int kk = (wave * kCopies + j) * (64 / kBChunks) + lane / kBChunks;
-    const int col = n0 + 8 * ((lane % kBChunks) ^ swizzle_b(kk));
-    b_dma[j] = kk * ldb * 2 + (min(col, ldb - 8) - n0) * 2;
+    const int col = n0 + Cfg::kChunkElems * ((lane % kBChunks) ^ Cfg::swizzle_b(kk));
+    b_dma[j] = kk * ldb * kSize + (min(col, ldb - Cfg::kChunkElems) - n0) * kSize;
   }
   // Bytes from a step's base to the end of its operand, capped at the
   // 32-bit range (every offset above stays far below it). Steps past the
@@ -581,18 +647,20 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
     return static_cast<unsigned>(bytes < 0xffffffffLL ? bytes : 0xffffffffLL);
   };
   // Operand origins of this tile's first K step (kstep0 > 0: a tail part).
-  const _Float16* const a_tile = A + static_cast<std::size_t>(m0) * K + kstep0 * kBK;
-  const _Float16* const b_tile = B + static_cast<std::size_t>(kstep0) * kBK * ldb + n0;
-  const long long a_total = static_cast<long long>(M - m0) * K * 2 - 2LL * kstep0 * kBK;
+  const T* const a_tile = A + static_cast<std::size_t>(m0) * K + kstep0 * kBK;
+  const T* const b_tile = B + static_cast<std::size_t>(kstep0) * kBK * ldb + n0;
+  const long long a_total =
+      static_cast<long long>(M - m0) * K * kSize - static_cast<long long>(kSize) * kstep0 * kBK;
   const long long b_total =
-      (static_cast<long long>(K) - static_cast<long long>(kstep0) * kBK) * ldb * 2 - 2LL * n0;
+      (static_cast<long long>(K) - static_cast<long long>(kstep0) * kBK) * ldb * kSize -
+      static_cast<long long>(kSize) * n0;
   auto issue = [&](unsigned char* stage, int kstep) {
     const int k0 = kstep * kBK;
     const unsigned live = kstep < steps ? ~0u : 0u;
-    const unsigned a_span = span(a_total - 2LL * k0) & live;
-    const unsigned b_span = span(b_total - 2LL * k0 * ldb) & live;
-    const _Float16* a_base = a_tile + k0;
-    const _Float16* b_base = b_tile + static_cast<std::size_t>(k0) * ldb;
+    const unsigned a_span = span(a_total - static_cast<long long>(kSize) * k0) & live;
+    const unsigned b_span = span(b_total - static_cast<long long>(kSize) * k0 * ldb) & live;
+    const T* a_base = a_tile + k0;
+    const T* b_base = b_tile + static_cast<std::size_t>(k0) * ldb;
 #pragma unroll
     for (int j = 0; j < kCopies; ++j) {
       opl::buffer_copy16_lds(a_base, a_span, stage + (wave * kCopies + j) * 1024,
@@ -602,13 +670,14 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
     }
   };
 
-  // Fragment byte offsets inside a stage (MFMA 16x16x32: lane l supplies
-  // row / column l % 16 and the 8-element k chunk l / 16 of a k32 substep).
+  // Fragment byte offsets inside a stage (lane l supplies row / column
+  // l % 16 of its operands and the 16-byte k chunk l / 16 of a substep).
   // A: row m = wm * BM / 2 + 16 ti + l % 16 has the same swizzle for every
-  // ti (rows 16 apart), so one VGPR per substep s serves every ti. B: k & 3
-  // and bit 3 of k are the same for every s and both 4-row halves, so one
-  // VGPR per tj serves every s and half.
-  constexpr int kBSubstep = 32 * Cfg::kBRowBytes;
+  // ti (rows 16 apart), so one VGPR per substep s serves every ti. B, fp16:
+  // k & 3 and bit 3 of k are the same for every s and both 4-row halves;
+  // fp32: rows 16 s + 4 group + e share the swizzle of row 4 group. Either
+  // way one VGPR per tj serves every s (and half, or e).
+  constexpr int kBSubstep = E::kSubK * Cfg::kBRowBytes;
   unsigned a_lane[Cfg::kSubsteps];
   {
     const int m = wm * (kBM / kWM) + gl;
@@ -619,9 +688,17 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   unsigned b_lane[kFN];
 #pragma unroll
   for (int tj = 0; tj < kFN; ++tj) {
-    const int n = wn * (kBN / kWN) + 16 * tj + 4 * (gl % 4);
-    const int k = 8 * group + gl / 4;
-    b_lane[tj] = kABytes + k * Cfg::kBRowBytes + (((n / 8) ^ swizzle_b(k)) * 16) + (n % 8) * 2;
+    if constexpr (kSize == 2) {
+      const int n = wn * (kBN / kWN) + 16 * tj + 4 * (gl % 4);
+      const int k = 8 * group + gl / 4;
+      b_lane[tj] = kABytes + k * Cfg::kBRowBytes + (((n / 8) ^ Cfg::swizzle_b(k)) * 16) +
+                   (n % 8) * 2;
+    } else {
+      const int n = wn * (kBN / kWN) + 16 * tj + gl;
+      const int k = 4 * group;
+      b_lane[tj] = kABytes + k * Cfg::kBRowBytes + (((n / 4) ^ Cfg::swizzle_b(k)) * 16) +
+                   (n % 4) * 4;
+    }
   }
 
   floatx4 acc[kFM][kFN];
@@ -635,48 +712,75 @@ void gemm_f16_dma_kernel(const _Float16* __restrict__ A,
   // Fragments of substep s, read in the order the MFMAs use them (ti-major):
   // A 0, every B, then the other A.
   auto load_a = [&](const unsigned char* st, int s, Fragments<Cfg>& f, int t) {
-    f.a[t] = *reinterpret_cast<const half8*>(st + a_lane[s] + t * 16 * Cfg::kARowBytes);
+    f.a[t] = *reinterpret_cast<const typename Cfg::Frag*>(st + a_lane[s] +
+                                                          t * 16 * Cfg::kARowBytes);
   };
   auto load = [&](const unsigned char* st, int s, Fragments<Cfg>& f) {
     load_a(st, s, f, 0);
 #pragma unroll
     for (int t = 0; t < kFN; ++t) {
-      const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-          (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s));
-      const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-          (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s + 4 * Cfg::kBRowBytes));
-      half8 b;
+      if constexpr (kSize == 2) {
+        const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s));
+        const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+            (OPL_LDS fp16x4*)(st + b_lane[t] + kBSubstep * s + 4 * Cfg::kBRowBytes));
+        half8 b;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        b[e] = lo[e];
-        b[4 + e] = hi[e];
+        for (int e = 0; e < 4; ++e) {
+          b[e] = lo[e];
+          b[4 + e] = hi[e];
+        }
+        f.b[t] = b;
+      } else {
+        const OPL_LDS unsigned char* bb =
+            (const OPL_LDS unsigned char*)(st + b_lane[t]) + kBSubstep * s;
+        floatx4 b;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          b[e] = *(const OPL_LDS float*)(bb + e * Cfg::kBRowBytes);
+        f.b[t] = b;
       }
-      f.b[t] = b;
     }
 #pragma unroll
     for (int t = 1; t < kFM; ++t) load_a(st, s, f, t);
   };
+  // fp32: the four k MFMAs of a block are kFM * kFN MFMAs apart.
   auto mma = [&](const Fragments<Cfg>& f) {
+    if constexpr (kSize == 2) {
 #pragma unroll
-    for (int ti = 0; ti < kFM; ++ti)
+      for (int ti = 0; ti < kFM; ++ti)
 #pragma unroll
-      for (int tj = 0; tj < kFN; ++tj)
-        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            f.a[ti], f.b[tj], acc[ti][tj], 0, 0, 0);
+        for (int tj = 0; tj < kFN; ++tj)
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              f.a[ti], f.b[tj], acc[ti][tj], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int ti = 0; ti < kFM; ++ti)
+#pragma unroll
+          for (int tj = 0; tj < kFN; ++tj)
+            acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                f.a[ti][e], f.b[tj][e], acc[ti][tj], 0, 0, 0);
+    }
   };
-  // Scheduling groups for one substep: each MFMA followed by its share of
-  // the LDS reads (the next substep's fragments) and, with_dma, of the DMA
-  // issues, spread evenly, so reads and copies issue in the MFMAs' shadow
-  // instead of in a burst.
-  constexpr int kMfmas = kFM * kFN;
-  static_assert(kMfmas >= kReads && kMfmas >= kIssues, "at most one read and copy per MFMA");
+  // Scheduling groups for one substep: each block's MFMAs (one fp16 MFMA,
+  // four fp32 ones) followed by their share of the LDS reads (the next
+  // substep's fragments) and, with_dma, of the DMA issues, spread evenly,
+  // so reads and copies issue in the MFMAs' shadow instead of in a burst.
+  // (fp32 groups of single MFMAs left 29 VGPRs spilled: the scheduler then
+  // stretched the accumulators' live ranges.)
+  constexpr int kGroups = kFM * kFN;
+  static_assert(2 * kGroups >= kReads && kGroups >= kIssues,
+                "at most two reads and one copy per group");
   auto interleave = [&](bool with_dma) {
 #pragma unroll
-    for (int i = 0; i < kMfmas; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      if ((i + 1) * kReads / kMfmas != i * kReads / kMfmas)
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      if (with_dma && (i + 1) * kIssues / kMfmas != i * kIssues / kMfmas)
+    for (int i = 0; i < kGroups; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, E::kMfmas, 0);  // MFMA
+      const int reads = (i + 1) * kReads / kGroups - i * kReads / kGroups;
+      if (reads >= 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (reads >= 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (with_dma && (i + 1) * kIssues / kGroups != i * kIssues / kGroups)
         __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // VMEM
     }
   };
@@ -1529,7 +1633,7 @@ int staging_for(const T* a, const T* b, int n, int k) {
 }
 
 template <typename Cfg>
-hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
+hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Type* b, float* c,
                             int m, int n, int k, int ldb, hipStream_t stream,
                             dma::TailSplit tail = {0, 0, 0, nullptr}) {
   const long long tiles = static_cast<long long>((m + Cfg::kBM - 1) / Cfg::kBM) *
@@ -1541,15 +1645,15 @@ hipError_t launch_dma_tiles(const _Float16* a, const _Float16* b, float* c,
     if (tail.splits > 0) return hipErrorInvalidValue;
   }
   if (tail.splits > 0) {
-    dma::gemm_f16_dma_kernel<Cfg, Cfg::kBM == 256><<<dim3(static_cast<unsigned>(blocks)),
-                                          dim3(Cfg::kThreads), 0, stream>>>(a, b, c, m, n, k,
-                                                                             ldb, tail);
+    dma::gemm_dma_kernel<Cfg, Cfg::kBM == 256><<<dim3(static_cast<unsigned>(blocks)),
+                                                 dim3(Cfg::kThreads), 0, stream>>>(
+        a, b, c, m, n, k, ldb, tail);
     if constexpr (Cfg::kBM == 256)
       dma::sum_tail_kernel<Cfg><<<dim3(Cfg::kBM * Cfg::kBN / 4 / 256, tail.tiles), dim3(256), 0,
                                   stream>>>(c, m, n, tail);
   } else {
-    dma::gemm_f16_dma_kernel<Cfg><<<dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads),
-                                    0, stream>>>(a, b, c, m, n, k, ldb, tail);
+    dma::gemm_dma_kernel<Cfg><<<dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads), 0,
+                                stream>>>(a, b, c, m, n, k, ldb, tail);
   }
   return hipGetLastError();
 }
@@ -1590,6 +1694,25 @@ int device_cus() {
 // 4096 (180) 102.8 vs 110.0; 4096^3 (256) 121.1 vs 136.5.
 constexpr long long kSmallGridTiles = 160;
 
+// The direct-to-LDS tile configurations of an element type, and the grid
+// (in 256 x 256 tiles) below which the 128 x 128 ones run.
+template <typename T>
+struct DmaTiles;
+template <>
+struct DmaTiles<_Float16> {
+  using Big = dma::BigTile;
+  using BigHalfK = dma::BigTileK32;  // K % 64 == 32
+  using Small = dma::SmallTile;
+  static constexpr long long kSmallBelow = kSmallGridTiles;
+};
+template <>
+struct DmaTiles<float> {
+  using Big = dma::BigTileF32;
+  using BigHalfK = dma::BigTileF32K16;  // K % 32 == 16
+  using Small = dma::SmallTileF32;
+  static constexpr long long kSmallBelow = kSmallGridTilesF32;
+};
+
 // Split of the last round of a 256 x 256-tile grid (splits == 0: none).
 struct TailPlan {
   int splits = 0;
@@ -1597,12 +1720,13 @@ struct TailPlan {
   std::size_t bytes = 0;
 };
 
+template <typename T>
 TailPlan tail_plan(int m, int n, int k, std::size_t capacity) {
   TailPlan t;
   const long long big_tiles =
       static_cast<long long>((m + dma::BigTile::kBM - 1) / dma::BigTile::kBM) *
       ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
-  if (big_tiles < kSmallGridTiles) return t;
+  if (big_tiles < DmaTiles<T>::kSmallBelow) return t;
   const int cus = device_cus();
   const long long last = cus > 0 ? big_tiles % cus : 0;
   if (cus <= 0 || big_tiles <= cus || last == 0 || last > cus / 2) return t;
@@ -1620,26 +1744,28 @@ TailPlan tail_plan(int m, int n, int k, std::size_t capacity) {
   return t;
 }
 
-// The direct-to-LDS kernel (k % dma::kBK == 0) on 128 x 128 or 256 x 256
+// The direct-to-LDS kernel (k % dma::kBK<T> == 0) on 128 x 128 or 256 x 256
 // tiles, with `tail` split into `partials` (tail.bytes of scratch).
-hipError_t launch_gemm_f16_dma(const _Float16* a, const _Float16* b, float* c,
-                               int m, int n, int k, int ldb, const TailPlan& tail,
-                               void* partials, hipStream_t stream) {
-  static_assert(dma::BigTile::kBM == dma::BigTileK32::kBM &&
-                    dma::BigTile::kBN == dma::BigTileK32::kBN,
+template <typename T>
+hipError_t launch_gemm_dma(const T* a, const T* b, float* c, int m, int n, int k, int ldb,
+                           const TailPlan& tail, void* partials, hipStream_t stream) {
+  using Tiles = DmaTiles<T>;
+  static_assert(Tiles::Big::kBM == dma::BigTile::kBM && Tiles::Big::kBN == dma::BigTile::kBN &&
+                    Tiles::BigHalfK::kBM == dma::BigTile::kBM &&
+                    Tiles::BigHalfK::kBN == dma::BigTile::kBN,
                 "one big tile size");
   const long long big_tiles =
       static_cast<long long>((m + dma::BigTile::kBM - 1) / dma::BigTile::kBM) *
       ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
-  if (big_tiles < kSmallGridTiles)
-    return launch_dma_tiles<dma::SmallTile>(a, b, c, m, n, k, ldb, stream);
+  if (big_tiles < Tiles::kSmallBelow)
+    return launch_dma_tiles<typename Tiles::Small>(a, b, c, m, n, k, ldb, stream);
   dma::TailSplit split{0, 0, 0, nullptr};
   if (tail.splits > 0)
     split = dma::TailSplit{static_cast<int>(big_tiles - tail.last), static_cast<int>(tail.last),
                            tail.splits, static_cast<float*>(partials)};
-  if (k % dma::BigTile::kBK == 0)
-    return launch_dma_tiles<dma::BigTile>(a, b, c, m, n, k, ldb, stream, split);
-  return launch_dma_tiles<dma::BigTileK32>(a, b, c, m, n, k, ldb, stream, split);
+  if (k % Tiles::Big::kBK == 0)
+    return launch_dma_tiles<typename Tiles::Big>(a, b, c, m, n, k, ldb, stream, split);
+  return launch_dma_tiles<typename Tiles::BigHalfK>(a, b, c, m, n, k, ldb, stream, split);
 }
 
 // One call's plan and the scratch it needs.
@@ -1663,19 +1789,21 @@ GemmPlan plan_gemm(const T* a, const T* b, int m, int n, int k, std::size_t capa
       return p;
     }
   }
+  // The copy kernel's per-lane offsets inside a tile are 32-bit: up to
+  // 255 rows of A (255 * K * sizeof(T) bytes) and one K step of B rows (64
+  // fp16 or 32 fp32 rows: 128 * N bytes).
+  const bool dma_offsets_fit = k < (sizeof(T) == 2 ? (1 << 22) : (1 << 21)) && n < (1 << 24);
+  constexpr int kChunkElems = 16 / static_cast<int>(sizeof(T));
+  if (dma_offsets_fit && k % dma::kBK<T> == 0 && n % kChunkElems == 0 && opl::aligned16(a) &&
+      opl::aligned16(b)) {
+    p.kind = GemmPlan::kDma;
+    p.tail = tail_plan<T>(m, n, k, capacity);
+    p.bytes = p.tail.bytes;
+    return p;
+  }
   if constexpr (std::is_same<T, _Float16>::value) {
-    // The copy kernel's per-lane offsets inside a tile are 32-bit: up to
-    // 255 rows of A (255 * K * 2 bytes) and 64 rows of B (64 * N * 2).
-    const bool dma_offsets_fit = k < (1 << 22) && n < (1 << 24);
-    if (dma_offsets_fit && k % dma::kBK == 0 && n % 8 == 0 && opl::aligned16(a) &&
-        opl::aligned16(b)) {
-      p.kind = GemmPlan::kDma;
-      p.tail = tail_plan(m, n, k, capacity);
-      p.bytes = p.tail.bytes;
-      return p;
-    }
     if (dma_offsets_fit && worth_padding(m, n, k)) {
-      const PadPlan pad = pad_plan<T>(a, b, m, n, k, dma::kBK, 8);
+      const PadPlan pad = pad_plan<T>(a, b, m, n, k, dma::kBK<T>, 8);
       if (pad.kp <= 0x7fffffffLL && pad.np <= 0x7fffffffLL && pad.bytes() <= capacity) {
         p.kind = GemmPlan::kPaddedDma;
         p.pad = pad;
@@ -1699,12 +1827,12 @@ hipError_t run_gemm(const GemmPlan& p, const T* a, const T* b, float* c, int m, 
       return skinny::launch<T>(a, b, c, m, n, k, p.skinny, scratch, lease, stream);
     case GemmPlan::kDma:
     case GemmPlan::kPaddedDma:
+      if (p.kind == GemmPlan::kDma)
+        return launch_gemm_dma<T>(a, b, c, m, n, k, n, p.tail, scratch, stream);
       if constexpr (std::is_same<T, _Float16>::value) {
-        if (p.kind == GemmPlan::kDma)
-          return launch_gemm_f16_dma(a, b, c, m, n, k, n, p.tail, scratch, stream);
         const PaddedOperands q = pad_into<T>(a, b, m, n, k, p.pad, scratch, stream);
-        return launch_gemm_f16_dma(static_cast<const T*>(q.a), static_cast<const T*>(q.b), c,
-                                   m, n, q.k, q.ldb, TailPlan{}, nullptr, stream);
+        return launch_gemm_dma<T>(static_cast<const T*>(q.a), static_cast<const T*>(q.b), c, m,
+                                  n, q.k, q.ldb, TailPlan{}, nullptr, stream);
       }
       return hipErrorInvalidValue;
     default:

@@ -507,6 +507,32 @@ def test_gemm_f16_step_counts(hip, mnk):
     assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize("mnk", [(4096, 4096, 1056), (4096, 4096, 32), (4096, 4096, 48),
+                                 (4096, 4096, 16), (4096, 4100, 256), (4100, 4096, 512),
+                                 (4096, 4160, 1024), (4160, 4096, 1040), (520, 2056, 1024),
+                                 (1000, 4100, 48), (600, 1100, 16), (1000, 700, 80),
+                                 (520, 2052, 112)])
+def test_gemm_f32_step_counts(hip, mnk):
+    """fp32 direct-to-LDS tiles over every step-count remainder of their
+    loops: 256 x 256 tiles with K % 32 == 0 run 32-deep steps in pairs (33
+    steps, a single step); with K % 32 == 16, 16-deep steps in fours (3
+    steps, 1 step); a ragged last tile column of one 4-column chunk and a
+    ragged last tile row; grids one round plus 16 tiles long whose last
+    round is split along K (2 parts, 4 parts of 8 steps, 4 uneven parts of
+    16-deep steps); 128 x 128 tiles on small grids (64, 3, 1, 5 and 7
+    steps, N off a multiple of 8)."""
+    m, n, k = mnk
+    a = oracle.uniform(690 + m, (m, k))
+    b = oracle.uniform(691 + n, (k, n))
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(m - 8, m),
+                                     sample_rows(m, 24, 692)]))
+    y = hip.gemm_f32(a, b)
+    ref = oracle.gemm(a, b, rows)
+    assert np.linalg.norm(y[rows] - ref) / np.linalg.norm(ref) <= 1e-4
+    assert np.all(np.abs(y[rows] - ref) <= 1e-3 + 1e-3 * np.abs(ref))
+    assert np.isfinite(y).all()
+
+
 def test_gemm_padded_then_smaller(hip):
     """The arena is reused: a large padded call followed by a smaller one
     and a larger one must all be right."""

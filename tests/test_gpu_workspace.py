@@ -6,8 +6,8 @@ point's bits; a workspace one byte short must be rejected before anything
 is enqueued (the output keeps its NaN fill). Cases: every launch sequence
 that uses scratch (reduce partials, decode split-K partials on both skinny
 kernels, padded fp16 operands at the 4095^3 BASELINE edge shape, the split
-last round of a 256 x 256-tile fp16 grid, split fp32 and fp16 register-
-staged attention).
+last round of 256 x 256-tile fp16 and fp32 grids, split fp32 and fp16
+register-staged attention).
 """
 
 from __future__ import annotations
@@ -64,12 +64,12 @@ def test_reduce_ws_matches_plain(lib, n):
 
 
 # (m, n, k, dtype): narrow decode shapes (split K) on both skinny kernels,
-# padded 1000^3 and
-# 4095^3 fp16, a 272-tile fp16 grid whose last round is split, an aligned
-# shape that needs no scratch.
+# padded 1000^3 and 4095^3 fp16, 272-tile fp16 and fp32 grids whose last
+# round is split, shapes that need no scratch.
 GEMM_CASES = [(1, 1024, 4096, "f16"), (16, 1024, 4096, "f16"), (1, 1024, 4096, "f32"),
               (16, 1024, 4096, "f32"), (1000, 1000, 1000, "f16"), (4095, 4095, 4095, "f16"),
-              (4352, 4096, 512, "f16"), (1024, 1024, 1024, "f16"), (999, 1001, 1003, "f32")]
+              (4352, 4096, 512, "f16"), (4352, 4096, 512, "f32"), (1024, 1024, 1024, "f16"),
+              (999, 1001, 1003, "f32")]
 
 
 @pytest.mark.parametrize("m,n,k,dtype", GEMM_CASES)

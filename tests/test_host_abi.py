@@ -192,8 +192,9 @@ def test_bench_refuses_more_than_one_gpu():
 # ------------------------------------------------------------- workspace forms
 # Queries and the *_ws entry points' workspace checks run before any HIP
 # call, so they are exercised here with fake (never dereferenced) pointers.
-# The shapes avoid the fp16 direct-to-LDS path, whose plan reads the CU
-# count from the runtime.
+# Shapes on the direct-to-LDS path split a grid's partly filled last round
+# by the CU count the runtime reports; without a GPU none is reported and
+# nothing is split, so these shapes avoid such rounds or that path.
 
 def test_reduce_workspace_size(lib):
     q = lib.operatorlib_reduce_sum_f32_workspace_size
@@ -216,7 +217,7 @@ def test_gemm_workspace_size(lib):
     assert f16(FAKE, FAKE, 4095, 4095, 4095) == (4095 * 4096 * 2 + 255) // 256 * 256 + 4096 * 4096 * 2
     # fp32 reads unaligned rows directly: never padded
     assert f32(FAKE, FAKE, 4095, 4095, 4095) == 0
-    assert f32(FAKE, FAKE, 4096, 4096, 4096) == 0
+    assert f32(FAKE, FAKE, 4096, 4096, 4096) == 0  # one whole round of 256 tiles
     assert f16(NULL, FAKE, 4095, 4095, 4095) == 0  # invalid arguments
 
 
