@@ -17,11 +17,11 @@
  * scratch beyond the caller's buffers (reduce partials, split-K partial
  * sums, padded GEMM operands, split attention partials) take it from one
  * of two places:
- *   - the plain entry points: a static array of 64 MiB per GPU (the
+ *   - the plain entry points: a static array of 256 MiB per GPU (the
  *     "arena"), held from the library's load to process exit. Calls that
  *     use it on different streams are ordered on the device by an event
  *     chain, so they stay safe across streams and host threads without
- *     blocking the host. A plan that would need more than 64 MiB uses
+ *     blocking the host. A plan that would need more than 256 MiB uses
  *     fewer splits or a kernel that needs none. Under stream capture the
  *     chain is not captured: replays of such a graph must not overlap
  *     another arena user on the same GPU (replay in stream order with the

@@ -49,9 +49,11 @@
 
 namespace opl {
 
-// Bytes of each GPU's arena. It holds the padded operands of an fp16 GEMM
-// up to 4096 x 4096 x 4096 and every other BASELINE-size plan in full.
-constexpr std::size_t kArenaBytes = std::size_t(64) << 20;
+// Bytes of each GPU's arena (under 0.1% of an MI355X's 288 GB). It holds
+// the padded operands of GEMMs up to 5120 x 5120 x 5120 in fp32 (200 MiB)
+// or 7168^3 in fp16, and every plan at the reference's benchmark sizes in
+// full, split last rounds included.
+constexpr std::size_t kArenaBytes = std::size_t(256) << 20;
 
 // Plans are computed for a scratch capacity: kUnlimited for workspace-size
 // queries and the *_ws entry points, kArenaBytes for the others.

@@ -533,6 +533,28 @@ def test_gemm_f32_step_counts(hip, mnk):
     assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize("mnk", [(4097, 4095, 4093), (4352, 4100, 999)])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_gemm_padded_split_tail(hip, mnk, dtype):
+    """Padded operands on a grid one round plus 16 (33) 256 x 256 tiles
+    long: the last round is split along K (16 parts; 3 parts) into partials
+    placed after the padded copies in the same scratch."""
+    m, n, k = mnk
+    a = oracle.uniform(640 + m, (m, k))
+    b = oracle.uniform(641 + n, (k, n))
+    rows = tile_row_rows(m, 642)
+    if dtype == "f16":
+        a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(a, b)
+        ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b), rows)
+        assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b)
+        ref = oracle.gemm(a, b, rows)
+        assert np.linalg.norm(y[rows] - ref) / np.linalg.norm(ref) <= 1e-4
+    assert np.isfinite(y).all()
+
+
 def test_gemm_padded_then_smaller(hip):
     """The arena is reused: a large padded call followed by a smaller one
     and a larger one must all be right."""

@@ -215,9 +215,11 @@ def test_gemm_workspace_size(lib):
     assert f16(FAKE, FAKE, 1, 1024, 4096) == 64 * 1 * 1024 * 4
     # 4095^3 fp16: A padded to [4095, 4096], B to [4096, 4096]
     assert f16(FAKE, FAKE, 4095, 4095, 4095) == (4095 * 4096 * 2 + 255) // 256 * 256 + 4096 * 4096 * 2
-    # fp32 reads unaligned rows directly: never padded
-    assert f32(FAKE, FAKE, 4095, 4095, 4095) == 0
+    # 4095^3 fp32: A padded to [4095, 4096], B to [4096, 4096]
+    assert f32(FAKE, FAKE, 4095, 4095, 4095) == 4095 * 4096 * 4 + 4096 * 4096 * 4
     assert f32(FAKE, FAKE, 4096, 4096, 4096) == 0  # one whole round of 256 tiles
+    # below 2^30 flop the register-staged kernel reads the operands in place
+    assert f32(FAKE, FAKE, 500, 500, 999) == 0
     assert f16(NULL, FAKE, 4095, 4095, 4095) == 0  # invalid arguments
 
 
