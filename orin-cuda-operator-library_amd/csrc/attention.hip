@@ -612,13 +612,15 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
 // Grids of fewer query blocks than this split each block's keys in two:
-// below 256 (a CU each) any grid gains; causal grids gain up to 384 blocks,
-// because the split halves the key walk of their heaviest blocks. Measured
-// on MI355X (us, unsplit vs split): B1 H12 S1024 22.1 vs 20.5 (causal 22.1
-// vs 20.7); B1 H12 S2048 39.9 vs 36.2; B1 H16 S2048 causal 39.8 vs 35.6;
-// B1 H12 S4096 causal 102.8 vs 77.2; B1 H32 S2048 (512 blocks) 77.5 vs
-// 85.0, causal 61.0 vs 63.6; B4 H32 S8192 causal 2238 vs 2408.
-constexpr long long kSplitKeysBelow = 256;
+// up to 256 (a CU each) any grid gains, as the unsplit block runs one
+// wavefront per SIMD; causal grids gain up to 384 blocks, because the split
+// halves the key walk of their heaviest blocks. Measured on MI355X (us,
+// unsplit vs split): B1 H12 S1024 22.1 vs 20.5 (causal 22.1 vs 20.7); B1
+// H12 S2048 39.9 vs 36.2; B1 H8 S4096 (256 blocks) 86.1 vs 72.3; B1 H16
+// S2048 42.1 vs 38.5, causal 39.8 vs 35.6; B1 H12 S4096 (384) 111.7 vs
+// 124.4, causal 102.8 vs 77.2; B1 H32 S2048 (512) 77.5 vs 85.0, causal
+// 61.0 vs 63.6; B4 H32 S8192 causal 2238 vs 2408.
+constexpr long long kSplitKeysBelow = 257;
 constexpr long long kSplitKeysBelowCausal = 512;
 // Grids of at most this many 128-row query blocks run 64-row blocks, so
 // that twice as many CUs share the work. Measured on MI355X (us, 128- vs

@@ -652,15 +652,16 @@ def test_attention_f16_small(hip, s, d, causal, extreme, offset):
     (1, 384, 128, True), (3, 384, 64, True), (9, 256, 128, False), (5, 128, 64, True),
     (128, 128, 128, True), (43, 384, 64, False), (168, 384, 64, True),
     (256, 256, 64, True),
-    # D 128, 128-row blocks, keys split (< 256 blocks, < 512 causal)
-    (50, 384, 128, False), (100, 384, 128, True),
+    # D 128, 128-row blocks, keys split (<= 256 blocks, < 512 causal)
+    (50, 384, 128, False), (100, 384, 128, True), (64, 512, 128, False),
     # 128-row blocks, keys not split
-    (512, 128, 128, False), (129, 384, 64, False), (171, 384, 64, True)])
+    (512, 128, 128, False), (86, 384, 128, False), (129, 384, 64, False),
+    (171, 384, 64, True)])
 def test_attention_f16_fast_path_covers_every_block(hip, heads, s, d, causal):
     # (heads x query blocks) not a multiple of 8: the work items are split
     # over 8 XCD ranges and the grid is padded; every row must be written.
-    # Small grids run 64-row blocks; mid-size D 128 grids (under 256 blocks,
-    # 512 causal) split each block's keys between two wavefront groups of
+    # Small grids run 64-row blocks; mid-size D 128 grids (up to 256 blocks,
+    # under 512 causal) split each block's keys between two wavefront groups of
     # the workgroup; larger ones do not.
     q, k, v = _attn_inputs(s, d, False, 970 + heads + s, heads=heads)
     qb, kb, vb = (oracle.to_f16_bits(t) for t in (q, k, v))
