@@ -650,25 +650,36 @@ static_assert(kHalfRowsUpToD64 >= kSplitKeysBelow - 1 &&
 // Headroom (log2 units) the running row max may lag the true max by.
 constexpr float kLazyLog2 = 8.0f;
 
-template <int D, int kTileKeys>
+// K/V tile layout in LDS for element type T (rows keep their global
+// layout, D elements each).
+template <typename T, int D, int kTileKeys>
 struct Layout {
-  static constexpr int kRowBytes = D * 2;
+  static constexpr int kSize = static_cast<int>(sizeof(T));
+  static constexpr int kElems = 16 / kSize;  // elements per 16-byte chunk
+  static constexpr int kRowBytes = D * kSize;
   static constexpr int kChunks = kRowBytes / 16;
   static constexpr int kTile = kTileKeys * kRowBytes;  // one K or V tile
   static constexpr int kStage = 2 * kTile;
-  static constexpr int kSteps = D / 32;    // QK^T k32 steps
+  // QK^T fragment steps over d: one 16-byte chunk per lane group covers 32
+  // fp16 dims (one MFMA 16x16x32) or 16 fp32 dims (four MFMA 16x16x4).
+  static constexpr int kSubK = 4 * kElems;
+  static constexpr int kSteps = D / kSubK;
   static constexpr int kDBlocks = D / 16;  // 16-dim blocks of O^T
   // K rows: 16 consecutive rows read one logical chunk (one 16-lane group)
   // and land on 16 different physical chunks.
   __device__ static int swizzle_k(int row) {
-    return D == 128 ? (row & 15) : ((row >> 1) & 7);
+    return kChunks >= 16 ? (row & 15) : ((row >> 1) & 7);
   }
-  // V rows: a ds_read_b64_tr_b16 group reads 8 bytes from each of 4 rows
-  // (4 lanes per row); the 4 rows, and the next group's 4, land on
-  // different banks.
+  // V rows, fp16: a ds_read_b64_tr_b16 group reads 8 bytes from each of 4
+  // rows (4 lanes per row); the 4 rows, and the next group's 4, land on
+  // different banks. fp32: each 16-lane group of a ds_read_b32 reads 64
+  // bytes of one row, the four groups rows 4 apart, which land on four
+  // different 64-byte bank ranges.
   __device__ static int swizzle_v(int row) {
-    return D == 128 ? ((4 * (row & 3)) ^ (2 * ((row >> 2) & 1)))
-                    : 2 * ((row >> 1) & 3);
+    if constexpr (kSize == 2)
+      return D == 128 ? ((4 * (row & 3)) ^ (2 * ((row >> 2) & 1))) : 2 * ((row >> 1) & 3);
+    else
+      return 4 * ((row >> 2) & 3);
   }
 };
 
@@ -698,15 +709,23 @@ struct HalfScores {
 // measured no faster on small grids (B1 H12 S1024: 20.9 us for both
 // against 20.5 us for two 64-key stages), so the tile loop is not waiting
 // on its copies; four groups, two wavefronts per SIMD, are what helps.
-template <int D, int kGroups, int kW, int kTileKeys>
+// fp32 rows are twice as long: its instances use 32-key tiles (64 KiB of
+// K/V stages per group at D = 128), and at most two groups.
+// Wavefronts per SIMD an instance must fit: one when four wavefronts hold
+// more than half a CU's LDS, else two.
+template <typename T, int D, int kGroups, int kW, int kTileKeys>
+constexpr int kMinWavesPerSimd =
+    2 * kGroups * Layout<T, D, kTileKeys>::kStage > 80 * 1024 && kGroups * kW == 4 ? 1 : 2;
+
+template <typename T, int D, int kGroups, int kW, int kTileKeys>
 __global__ __launch_bounds__(kW * opl::kWaveSize * kGroups)
-__attribute__((amdgpu_waves_per_eu(D == 128 && kW == 2 && kGroups == 2 ? 1 : 2, 2)))
-void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
-                              const _Float16* __restrict__ K,
-                              const _Float16* __restrict__ V,
-                              float* __restrict__ O, int BH, int S, int causal,
-                              float score_scale_log2) {
-  using L = Layout<D, kTileKeys>;
+__attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<T, D, kGroups, kW, kTileKeys>, 2)))
+void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
+                          const T* __restrict__ V, float* __restrict__ O, int BH, int S,
+                          int causal, float score_scale_log2) {
+  using L = Layout<T, D, kTileKeys>;
+  constexpr bool kHalf = L::kSize == 2;
+  using Frag = typename std::conditional<kHalf, half8, floatx4>::type;
   static_assert(kGroups == 1 || kGroups == 2 || kGroups == 4, "1, 2 or 4 key groups");
   static_assert(kW == 2 || kW == 4, "2 or 4 wavefronts per group");
   static_assert(kTileKeys == 32 || kTileKeys == 64, "32- or 64-key tiles");
@@ -750,20 +769,20 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   const int quad = lane / 16;
   const int wave_row0 = q0 + wave * kRowsPerWave;
   const std::size_t head = static_cast<std::size_t>(bh) * S * D;
-  const _Float16* qh = Q + head;
-  const _Float16* kh = K + head;
-  const _Float16* vh = V + head;
+  const T* qh = Q + head;
+  const T* kh = K + head;
+  const T* vh = V + head;
 
-  // Q^T operand of query block qc: query wave_row0 + 16 qc + col, dims
-  // 32 c + 8 quad .. + 7.
-  half8 qf[2][L::kSteps];
+  // Q^T operand of query block qc: query wave_row0 + 16 qc + col, the
+  // 16-byte chunk quad of step c (dims kSubK c + kElems quad ..).
+  Frag qf[2][L::kSteps];
 #pragma unroll
   for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
     for (int c = 0; c < L::kSteps; ++c)
-      qf[qc][c] = *reinterpret_cast<const half8*>(
+      qf[qc][c] = *reinterpret_cast<const Frag*>(
           qh + static_cast<std::size_t>(min(wave_row0 + 16 * qc + col, S - 1)) * D +
-          32 * c + 8 * quad);
+          L::kSubK * c + L::kElems * quad);
 
   // DMA: element offset of the chunk this lane copies, per copy.
   int k_src[kCopies], v_src[kCopies];
@@ -772,22 +791,22 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     const int slot = (wave * kCopies + j) * 64 + lane;
     const int row = slot / L::kChunks;
     const int phys = slot % L::kChunks;
-    k_src[j] = row * D + 8 * (phys ^ L::swizzle_k(row));
-    v_src[j] = row * D + 8 * (phys ^ L::swizzle_v(row));
+    k_src[j] = row * D + L::kElems * (phys ^ L::swizzle_k(row));
+    v_src[j] = row * D + L::kElems * (phys ^ L::swizzle_v(row));
   }
   // Buffer resources over the rest of this head's K and V from the tile's
-  // first key (the launcher guarantees S * D * 2 < 2^32): the per-lane byte
+  // first key (the launcher guarantees S * D * sizeof(T) < 2^32): the per-lane byte
   // offsets stay in 32-bit VGPRs and the base is scalar, so a tile's copies
   // cost no vector address arithmetic. The hardware range-checks only the
   // per-lane offset against the resource's size (the scalar offset is
   // exempt), so the tile's position goes into the base, not the scalar
   // offset: keys from S on then fall outside the range and read zeros,
   // never the next head or memory past the tensor.
-  const unsigned head_bytes = static_cast<unsigned>(S) * D * 2u;
+  const unsigned head_bytes = static_cast<unsigned>(S) * D * L::kSize;
 #pragma unroll
   for (int j = 0; j < kCopies; ++j) {
-    k_src[j] *= 2;  // elements -> bytes
-    v_src[j] *= 2;
+    k_src[j] *= L::kSize;  // elements -> bytes
+    v_src[j] *= L::kSize;
   }
   // The copies' LDS destinations (M0) are wave-uniform: derived from a
   // scalar copy of the wave index, they stay in scalar registers instead of
@@ -795,7 +814,7 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto issue = [&](unsigned char* st, int key0) {
     // key0 < S for every issued tile, so 0 < rest <= head_bytes < 2^32
-    const unsigned tile_bytes = static_cast<unsigned>(key0) * D * 2u;
+    const unsigned tile_bytes = static_cast<unsigned>(key0) * D * L::kSize;
     const unsigned rest = head_bytes - tile_bytes;
     const std::size_t tile_elems = static_cast<std::size_t>(key0) * D;
 #pragma unroll
@@ -813,17 +832,26 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
 #pragma unroll
   for (int c = 0; c < L::kSteps; ++c)
     k_off[c] = col * L::kRowBytes + (((4 * c + quad) ^ L::swizzle_k(col)) * 16);
-  // V^T operand of dim block db: lane l addresses 4 dims (16 db + 4 (col %
-  // 4) ..) of key row 4 quad + col / 4 and receives dim 16 db + col of key
-  // rows 4 quad + 0..3 (k slots 8 quad + 0..3); the read 16 rows on gives
-  // slots 8 quad + 4..7. That is the key order of the P^T registers below.
+  // V^T operand of dim block db. fp16: lane l addresses 4 dims (16 db + 4
+  // (col % 4) ..) of key row 4 quad + col / 4 and receives dim 16 db + col
+  // of key rows 4 quad + 0..3 (k slots 8 quad + 0..3); the read 16 rows on
+  // gives slots 8 quad + 4..7. fp32: lane l reads dim 16 db + col of key
+  // row 4 quad + e for MFMA e (rows 4 quad + e share row 4 quad's
+  // swizzle). Either way that is the key order of the P^T registers below.
   int v_base[L::kDBlocks];
 #pragma unroll
   for (int db = 0; db < L::kDBlocks; ++db) {
-    const int row = 4 * quad + col / 4;
-    const int d = 16 * db + 4 * (col % 4);
-    v_base[db] = L::kTile + row * L::kRowBytes +
-                 (((d >> 3) ^ L::swizzle_v(row)) * 16) + (d & 7) * 2;
+    if constexpr (kHalf) {
+      const int row = 4 * quad + col / 4;
+      const int d = 16 * db + 4 * (col % 4);
+      v_base[db] = L::kTile + row * L::kRowBytes +
+                   (((d >> 3) ^ L::swizzle_v(row)) * 16) + (d & 7) * 2;
+    } else {
+      const int row = 4 * quad;
+      const int d = 16 * db + col;
+      v_base[db] = L::kTile + row * L::kRowBytes +
+                   (((d >> 2) ^ L::swizzle_v(row)) * 16) + (d & 3) * 4;
+    }
   }
 
   // O^T of query block qc, dim block db: lane l holds query 16 qc + col,
@@ -845,11 +873,15 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
   // sum of its query row's p (as rounded to fp16 for P.V) in all four
   // elements. That replaces 32 VALU adds per tile and a wavefront with 4
   // MFMAs (the vector ALUs, not the matrix cores, are the busier pipe).
+  // fp32 keeps them on the vector ALUs instead (the matrix cores are its
+  // busier pipe): each lane sums its 8 of the row's p per 32 keys, and the
+  // four lanes of a row are combined once, after the loop.
   floatx4 sums[2];
 #pragma unroll
   for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
     for (int e = 0; e < 4; ++e) sums[qc][e] = 0.0f;
+  float lane_sum[2] = {0.0f, 0.0f};
   half8 ones;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones[e] = static_cast<_Float16>(1.0f);
@@ -884,25 +916,46 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
           for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
             for (int e = 0; e < 4; ++e) s.v[kb][qc][e] = 0.0f;
-        half8 a[2][L::kSteps];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int c = 0; c < L::kSteps; ++c)
-            a[kb][c] = *reinterpret_cast<const half8*>(
-                cur + k_off[c] + (32 * j + 16 * kb) * L::kRowBytes);
-        // All K reads of the half are issued before the MFMAs: with one
-        // workgroup per CU (small grids) nothing else hides their latency.
-        __builtin_amdgcn_sched_barrier(0);
-        // Four independent accumulators, so no MFMA waits on the previous.
-#pragma unroll
-        for (int c = 0; c < L::kSteps; ++c)
+        if constexpr (kHalf) {
+          half8 a[2][L::kSteps];
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int qc = 0; qc < 2; ++qc)
-              s.v[kb][qc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                  a[kb][c], qf[qc][c], s.v[kb][qc], 0, 0, 0);
+            for (int c = 0; c < L::kSteps; ++c)
+              a[kb][c] = *reinterpret_cast<const half8*>(
+                  cur + k_off[c] + (32 * j + 16 * kb) * L::kRowBytes);
+          // All K reads of the half are issued before the MFMAs: with one
+          // workgroup per CU (small grids) nothing else hides their latency.
+          __builtin_amdgcn_sched_barrier(0);
+          // Four independent accumulators, so no MFMA waits on the previous.
+#pragma unroll
+          for (int c = 0; c < L::kSteps; ++c)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+              for (int qc = 0; qc < 2; ++qc)
+                s.v[kb][qc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    a[kb][c], qf[qc][c], s.v[kb][qc], 0, 0, 0);
+        } else {
+          // fp32: 16 MFMAs per 16-dim step (4 dims x 2 key blocks x 2
+          // query blocks) hide the next step's two K reads.
+#pragma unroll
+          for (int c = 0; c < L::kSteps; ++c) {
+            floatx4 a[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+              a[kb] = *reinterpret_cast<const floatx4*>(
+                  cur + k_off[c] + (32 * j + 16 * kb) * L::kRowBytes);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+              for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int qc = 0; qc < 2; ++qc)
+                  s.v[kb][qc] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                      a[kb][e], qf[qc][c][e], s.v[kb][qc], 0, 0, 0);
+          }
+        }
         return s;
       };
       auto mask = [&](HalfScores& s, int j) {
@@ -951,47 +1004,81 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
           const float alpha = opl::fast_exp2(row_max[qc] - new_max);
           row_max[qc] = new_max;
           move_above[qc] = (new_max + kLazyLog2) * inv_scale;
+          if constexpr (kHalf) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sums[qc][e] *= alpha;
+            for (int e = 0; e < 4; ++e) sums[qc][e] *= alpha;
+          } else {
+            lane_sum[qc] *= alpha;
+          }
 #pragma unroll
           for (int db = 0; db < L::kDBlocks; ++db)
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[qc][db][e] *= alpha;
         }
       };
-      // P of query block qc as the B operand of P.V: k slots 8 quad + e are
-      // keys 4 quad + e of block 0, slots 8 quad + 4 + e those of block 1.
-      auto exponentiate = [&](const HalfScores& s, half8 (&pb)[2]) {
+      // P of query block qc as the B operand of P.V. fp16: k slots 8 quad
+      // + e are keys 4 quad + e of block 0, slots 8 quad + 4 + e those of
+      // block 1. fp32: [qc][kb][e] is key 16 kb + 4 quad + e, the operand of
+      // MFMA e over key block kb; the lane's sum of them is kept.
+      using PHalf = typename std::conditional<kHalf, half8[2], floatx4[2][2]>::type;
+      auto exponentiate = [&](const HalfScores& s, PHalf& pb) {
 #pragma unroll
         for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              pb[qc][4 * kb + e] = static_cast<_Float16>(opl::fast_exp2(
-                  fmaf(s.v[kb][qc][e], score_scale_log2, -row_max[qc])));
+            for (int e = 0; e < 4; ++e) {
+              const float p = opl::fast_exp2(
+                  fmaf(s.v[kb][qc][e], score_scale_log2, -row_max[qc]));
+              if constexpr (kHalf) {
+                pb[qc][4 * kb + e] = static_cast<_Float16>(p);
+              } else {
+                pb[qc][kb][e] = p;
+                lane_sum[qc] += p;
+              }
+            }
       };
-      auto accumulate = [&](int j, const half8 (&pb)[2]) {
+      auto accumulate = [&](int j, const PHalf& pb) {
         const int rows = 32 * j * L::kRowBytes;
+        if constexpr (!kHalf) {
+          // Each O^T accumulator is reused 16 MFMAs after its last update.
 #pragma unroll
-        for (int db = 0; db < L::kDBlocks; ++db) {
-          const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-              (OPL_LDS fp16x4*)(cur + v_base[db] + rows));
-          const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-              (OPL_LDS fp16x4*)(cur + v_base[db] + rows + 16 * L::kRowBytes));
-          half8 a;
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            a[e] = lo[e];
-            a[4 + e] = hi[e];
+            for (int e = 0; e < 4; ++e) {
+              float va[L::kDBlocks];
+#pragma unroll
+              for (int db = 0; db < L::kDBlocks; ++db)
+                va[db] = *reinterpret_cast<const float*>(
+                    cur + v_base[db] + rows + (16 * kb + e) * L::kRowBytes);
+#pragma unroll
+              for (int db = 0; db < L::kDBlocks; ++db)
+#pragma unroll
+                for (int qc = 0; qc < 2; ++qc)
+                  o[qc][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[db], pb[qc][kb][e],
+                                                                   o[qc][db], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+          for (int db = 0; db < L::kDBlocks; ++db) {
+            const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (OPL_LDS fp16x4*)(cur + v_base[db] + rows));
+            const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (OPL_LDS fp16x4*)(cur + v_base[db] + rows + 16 * L::kRowBytes));
+            half8 a;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              a[e] = lo[e];
+              a[4 + e] = hi[e];
+            }
+#pragma unroll
+            for (int qc = 0; qc < 2; ++qc)
+              o[qc][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[qc], o[qc][db], 0, 0, 0);
           }
 #pragma unroll
           for (int qc = 0; qc < 2; ++qc)
-            o[qc][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[qc], o[qc][db], 0, 0, 0);
+            sums[qc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[qc], sums[qc], 0, 0, 0);
         }
-#pragma unroll
-        for (int qc = 0; qc < 2; ++qc)
-          sums[qc] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[qc], sums[qc], 0, 0, 0);
       };
       // One rescale decision per tile, taken on both halves' maxima before
       // either P.V: the O rescale then happens in O's own registers (a
@@ -1001,7 +1088,7 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
       // the matrix cores, 2075 us.
       auto body = [&](auto masked_tag) {
         constexpr bool kMasked = decltype(masked_tag)::value;
-        half8 p0[2], p1[2];
+        PHalf p0, p1;
         // The QK^T MFMAs of both halves issue at raised wave priority: the
         // SIMD's other wavefront, usually in its exponentials then, yields
         // issue slots to them, so the two wavefronts' matrix and vector
@@ -1050,7 +1137,14 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
     tile(st1, st0, i + 1);
   }
   if (i < iters) tile(st0, st1, i);
-  float row_sum[2] = {sums[0][0], sums[1][0]};
+  float row_sum[2];
+#pragma unroll
+  for (int qc = 0; qc < 2; ++qc) {
+    if constexpr (kHalf)
+      row_sum[qc] = sums[qc][0];
+    else  // the four lanes of the row: l, l ^ 16, l ^ 32, l ^ 48
+      row_sum[qc] = opl::sum_lane_xor32(opl::combine_xor16_f32<opl::SumOp>(lane_sum[qc]));
+  }
 
   // After the loop every stage is free (the last iteration ended with a
   // barrier and issued no copy). Merge and staging blocks tile the two
@@ -1190,12 +1284,12 @@ void attention_f16_dma_kernel(const _Float16* __restrict__ Q,
 #undef OPL_LDS
 }  // namespace dma
 
-// True when the fp16 fast path applies.
-inline bool f16_dma_ok(const void* q, const void* k, const void* v,
-                       const void* out, int sequence, int head_dim) {
+// True when the fast path applies (head_dim 64 or 128, aligned tensors).
+inline bool dma_ok(const void* q, const void* k, const void* v, const void* out,
+                   int sequence, int head_dim, unsigned element_bytes) {
   // one head of K or V must be addressable with 32-bit buffer offsets
   const unsigned long long head_bytes =
-      static_cast<unsigned long long>(sequence) * head_dim * 2ull;
+      static_cast<unsigned long long>(sequence) * head_dim * element_bytes;
   return (head_dim == 64 || head_dim == 128) && head_bytes < (1ull << 32) &&
          opl::aligned16(q) && opl::aligned16(k) && opl::aligned16(v) &&
          opl::aligned16(out);
@@ -1218,51 +1312,74 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
                          opl::aligned16(out);
   hipStream_t stream = static_cast<hipStream_t>(stream_handle);
   const int c = causal ? 1 : 0;
-  if constexpr (sizeof(T) == 2) {
-    if (f16_dma_ok(q, k, v, out, sequence, head_dim)) {
-      if (query != nullptr) {  // the fast path needs no scratch
-        *query = 0;
-        return hipSuccess;
-      }
-      const float scale =
-          1.4426950408889634f / sqrtf(static_cast<float>(head_dim));
-      // Grids too small to fill the CUs split each query block's keys
-      // between groups of wavefronts in the workgroup; the smallest also
-      // halve the query block, and at D = 128 split its keys four ways.
-      const long long half_up_to =
-          head_dim == 128 ? dma::kHalfRowsUpTo
-                          : (causal ? dma::kHalfRowsUpToD64Causal : dma::kHalfRowsUpToD64);
-      const bool half_rows = blocks <= half_up_to;
-      const bool split = half_rows ||
-          blocks < (causal ? dma::kSplitKeysBelowCausal : dma::kSplitKeysBelow);
-      const long long wgs = half_rows ? 2 * blocks : blocks;
-      // a multiple of 8 workgroups, one contiguous range of work per XCD
-      const long long padded = (wgs + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
-      const dim3 grid(static_cast<unsigned>(padded));
+  if (dma_ok(q, k, v, out, sequence, head_dim, sizeof(T))) {
+    if (query != nullptr) {  // the fast path needs no scratch
+      *query = 0;
+      return hipSuccess;
+    }
+    const float scale = 1.4426950408889634f / sqrtf(static_cast<float>(head_dim));
+    // Grids too small to fill the CUs split each query block's keys
+    // between groups of wavefronts in the workgroup; the smallest also
+    // halve the query block (and, fp16 at D = 128, split its keys four ways).
+    const long long half_up_to =
+        head_dim == 128 ? dma::kHalfRowsUpTo
+                        : (causal ? dma::kHalfRowsUpToD64Causal : dma::kHalfRowsUpToD64);
+    const bool half_rows = blocks <= half_up_to;
+    const bool split = half_rows ||
+        blocks < (causal ? dma::kSplitKeysBelowCausal : dma::kSplitKeysBelow);
+    const long long wgs = half_rows ? 2 * blocks : blocks;
+    // a multiple of 8 workgroups, one contiguous range of work per XCD
+    const long long padded = (wgs + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
+    const dim3 grid(static_cast<unsigned>(padded));
+    if constexpr (sizeof(T) == 2) {
       if (head_dim == 128) {
         // 64-row blocks x 4 groups / 128-row blocks x 2 groups: 8 wavefronts
         const dim3 block(split ? 2 * kThreads : kThreads);
         if (half_rows)
-          dma::attention_f16_dma_kernel<128, 4, 2, 32><<<grid, block, 0, stream>>>(
+          dma::attention_dma_kernel<T, 128, 4, 2, 32><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else if (split)
-          dma::attention_f16_dma_kernel<128, 2, 4, 64><<<grid, block, 0, stream>>>(
+          dma::attention_dma_kernel<T, 128, 2, 4, 64><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else
-          dma::attention_f16_dma_kernel<128, 1, 4, 64><<<grid, block, 0, stream>>>(
+          dma::attention_dma_kernel<T, 128, 1, 4, 64><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
       } else {
         // (split implies half_rows at D = 64; 4 wavefronts either way)
         const dim3 block(kThreads);
         if (half_rows)
-          dma::attention_f16_dma_kernel<64, 2, 2, 64><<<grid, block, 0, stream>>>(
+          dma::attention_dma_kernel<T, 64, 2, 2, 64><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
         else
-          dma::attention_f16_dma_kernel<64, 1, 4, 64><<<grid, block, 0, stream>>>(
+          dma::attention_dma_kernel<T, 64, 1, 4, 64><<<grid, block, 0, stream>>>(
               q, k, v, out, bh, sequence, c, scale);
       }
-      return hipGetLastError();
+    } else {
+      // fp32: 32-key tiles, at most two groups (a group's K/V stages hold
+      // 64 KiB at D = 128): 64-row blocks with two groups of 2 wavefronts,
+      // 128-row blocks with two groups of 4, or one group of 4.
+      if (head_dim == 128) {
+        const dim3 block(split && !half_rows ? 2 * kThreads : kThreads);
+        if (half_rows)
+          dma::attention_dma_kernel<T, 128, 2, 2, 32><<<grid, block, 0, stream>>>(
+              q, k, v, out, bh, sequence, c, scale);
+        else if (split)
+          dma::attention_dma_kernel<T, 128, 2, 4, 32><<<grid, block, 0, stream>>>(
+              q, k, v, out, bh, sequence, c, scale);
+        else
+          dma::attention_dma_kernel<T, 128, 1, 4, 32><<<grid, block, 0, stream>>>(
+              q, k, v, out, bh, sequence, c, scale);
+      } else {
+        const dim3 block(kThreads);
+        if (half_rows)
+          dma::attention_dma_kernel<T, 64, 2, 2, 32><<<grid, block, 0, stream>>>(
+              q, k, v, out, bh, sequence, c, scale);
+        else
+          dma::attention_dma_kernel<T, 64, 1, 4, 32><<<grid, block, 0, stream>>>(
+              q, k, v, out, bh, sequence, c, scale);
+      }
     }
+    return hipGetLastError();
   }
   const int ndt = (head_dim + 31) / 32;
   SplitPlan plan;

@@ -691,6 +691,27 @@ def test_attention_f16_fast_path_ragged_sequence(hip, heads, s, d, causal):
     assert np.max(np.abs(y - ref)) <= 2e-3
 
 
+@pytest.mark.parametrize("heads,s,d,causal", [
+    # 64-row blocks, keys split between two groups (D 128 up to 128 blocks,
+    # D 64 up to 384 / 512 causal), several tiles per group
+    (2, 333, 128, True), (3, 100, 128, False), (4, 1000, 128, False), (2, 2000, 128, True),
+    (3, 65, 64, True), (100, 100, 64, False),
+    # D 128, 128-row blocks, keys split (<= 256 blocks, < 512 causal)
+    (200, 100, 128, False), (300, 100, 128, True),
+    # 128-row blocks, keys not split
+    (260, 100, 128, False), (520, 100, 128, True), (390, 100, 64, False),
+    (520, 100, 64, True)])
+def test_attention_f32_fast_path(hip, heads, s, d, causal):
+    """fp32 on the direct-to-LDS kernel (D 64 / 128, aligned tensors): every
+    instance, ragged sequence lengths (keys past S read zeros and are
+    masked, rows past S are not stored), every row against the oracle."""
+    q, k, v = _attn_inputs(s, d, False, 1010 + heads + s, heads=heads)
+    ref = oracle.attention(q, k, v, causal)
+    y = hip.attention(q, k, v, causal)
+    assert np.isfinite(y).all()
+    assert np.all(np.abs(y - ref) <= 1e-4 + 1e-4 * np.abs(ref))
+
+
 # (heads, S, D, causal) on every fp16 fast-path instance with S ragged:
 # D 128 64-row blocks / 128-row blocks with keys split / unsplit, D 64
 # 64-row blocks / 128-row blocks.

@@ -8,8 +8,8 @@ library together):
   * gemm_f16 1 x 1024 x 4096 (decode GEMM, split-K partials + split sum);
   * gemm_f16 1000^3 (K and N not multiples of the fast kernel's steps:
     zero-padded operand copies, then the product);
-  * attention_f32 B1 H4 S256 D128 (small grid: keys split over workgroups,
-    partials, then the combine kernel);
+  * attention_f32 B1 H4 S256 D96 (register-staged on a small grid: keys
+    split over workgroups, partials, then the combine kernel);
   * gemm_f16 4352 x 4096 x 512 (272 tiles of 256 x 256: the last round's 16
     tiles are split along K, partial tiles, then the tail sum).
 All of them take their scratch from the GPU's arena, which every stream
@@ -53,6 +53,10 @@ HIP_STREAM_PER_THREAD = 2  # hipStreamPerThread, include/hip/hip_runtime_api.h
 # every 256-row tile row, its first and last.
 TAIL_MK = (4352, 512)
 TAIL_N = 4096
+# attention head dim: 96 takes the register-staged kernel, whose small
+# grids split keys over workgroups through scratch (64 and 128 on aligned
+# tensors take the direct-to-LDS kernel, which needs none)
+ATTN_D = 96
 TAIL_ROWS = np.array(sorted({r for t in range(0, TAIL_MK[0], 256) for r in (t, t + 255)}),
                      dtype=np.int32)
 
@@ -66,7 +70,7 @@ class Case:
         self.b1 = oracle.to_f16_bits(oracle.uniform(seed + 2, (4096, SKINNY_N)))
         self.ap = oracle.to_f16_bits(oracle.uniform(seed + 3, (1000, 1000)))
         self.bp = oracle.to_f16_bits(oracle.uniform(seed + 4, (1000, 1000)))
-        self.q, self.k, self.v = (oracle.normal(seed + 5 + i, (1, 4, 256, 128)) for i in range(3))
+        self.q, self.k, self.v = (oracle.normal(seed + 5 + i, (1, 4, 256, ATTN_D)) for i in range(3))
         self.at = oracle.to_f16_bits(oracle.uniform(seed + 8, TAIL_MK))
         self.bt = oracle.to_f16_bits(oracle.uniform(seed + 9, (TAIL_MK[1], TAIL_N)))
         f = oracle.from_f16_bits
@@ -83,7 +87,7 @@ class Case:
             "reduce": torch.full((rounds,), float("nan"), device="cuda"),
             "skinny": torch.full((rounds, 1, SKINNY_N), float("nan"), device="cuda"),
             "padded": torch.full((rounds, 1000, 1000), float("nan"), device="cuda"),
-            "attn": torch.full((rounds, 1, 4, 256, 128), float("nan"), device="cuda"),
+            "attn": torch.full((rounds, 1, 4, 256, ATTN_D), float("nan"), device="cuda"),
             "tail": torch.full((rounds, TAIL_MK[0], TAIL_N), float("nan"), device="cuda"),
         }
 
@@ -96,7 +100,7 @@ class Case:
         check(lib.operatorlib_gemm_f16(ptr(d["ap"]), ptr(d["bp"]), ptr(o["padded"][r]),
                                        1000, 1000, 1000, stream), "gemm_f16 padded")
         check(lib.operatorlib_attention_f32(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),
-                                            ptr(o["attn"][r]), 1, 4, 256, 128, 0, stream),
+                                            ptr(o["attn"][r]), 1, 4, 256, ATTN_D, 0, stream),
               "attention_f32")
         check(lib.operatorlib_gemm_f16(ptr(d["at"]), ptr(d["bt"]), ptr(o["tail"][r]),
                                        TAIL_MK[0], TAIL_N, TAIL_MK[1], stream),
@@ -113,7 +117,7 @@ class Case:
             lib.operatorlib_gemm_f16_workspace_size(ptr(d["ap"]), ptr(d["bp"]), 1000, 1000,
                                                     1000),
             lib.operatorlib_attention_f32_workspace_size(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),
-                                                         ptr(tmp), 1, 4, 256, 128, 0),
+                                                         ptr(tmp), 1, 4, 256, ATTN_D, 0),
             lib.operatorlib_gemm_f16_workspace_size(ptr(d["at"]), ptr(d["bt"]), TAIL_MK[0],
                                                     TAIL_N, TAIL_MK[1]))
 
@@ -129,7 +133,7 @@ class Case:
         check(lib.operatorlib_gemm_f16_ws(ptr(d["ap"]), ptr(d["bp"]), ptr(o["padded"][r]),
                                           1000, 1000, 1000, w, nb, stream), "gemm_f16_ws padded")
         check(lib.operatorlib_attention_f32_ws(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),
-                                               ptr(o["attn"][r]), 1, 4, 256, 128, 0, w, nb,
+                                               ptr(o["attn"][r]), 1, 4, 256, ATTN_D, 0, w, nb,
                                                stream), "attention_f32_ws")
         check(lib.operatorlib_gemm_f16_ws(ptr(d["at"]), ptr(d["bt"]), ptr(o["tail"][r]),
                                           TAIL_MK[0], TAIL_N, TAIL_MK[1], w, nb, stream),
