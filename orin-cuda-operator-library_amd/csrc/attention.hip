@@ -611,6 +611,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 #define OPL_LDS __attribute__((address_space(3)))
 
 constexpr int kXcds = 8;
+// Workgroup slots of an XCD the causal work order is balanced over (32 CUs,
+// two workgroups each). Simulated greedy dispatch over 64 slots, B4 H32
+// S2048 causal (16 blocks per head of 4..64 32-key tiles, 256 per XCD):
+// head-major order finishes at 172 tile-times per slot against the 136
+// average; groups of 4 heads, heaviest first, at 136.
+constexpr int kCausalGroupSlots = 64;
 // Grids of fewer query blocks than this split each block's keys in two:
 // up to 256 (a CU each) any grid gains, as the unsplit block runs one
 // wavefront per SIMD; causal grids gain up to 384 blocks, because the split
@@ -751,8 +757,26 @@ void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   const int w = static_cast<int>(blockIdx.x % kXcds) * per_xcd +
                 static_cast<int>(blockIdx.x / kXcds);
   if (w >= total) return;  // padding of the grid to a multiple of 8
-  const int bh = w / q_blocks;
-  const int qb = q_blocks - 1 - w % q_blocks;
+  int bh = w / q_blocks;
+  int qb = q_blocks - 1 - w % q_blocks;
+  // Causal grids with few query blocks per head: a head's blocks (heaviest
+  // first) are too few for an XCD's workgroup slots to even out, and the
+  // heavy first blocks of the last heads start late. Groups of g heads,
+  // g * q_blocks about the slots of an XCD, are taken heaviest first
+  // across the group instead (block q_blocks - 1 of each head, then the
+  // next): the order a longest-first schedule of the group would use, with
+  // as many heads in flight per XCD as before. g = 1 (64 or more blocks
+  // per head) keeps the head-major order.
+  if (causal) {
+    const int g = max(1, kCausalGroupSlots / q_blocks);
+    if (g > 1) {
+      const int first = w / (g * q_blocks) * g;  // first head of w's group
+      const int heads = min(g, BH - first);
+      const int r = w - first * q_blocks;        // < heads * q_blocks
+      bh = first + r % heads;
+      qb = q_blocks - 1 - r / heads;
+    }
+  }
   const int q0 = qb * kRows;
   const int lane = threadIdx.x % opl::kWaveSize;
   // (Kept as a vector value: declaring it wave-uniform turns the causal
