@@ -136,7 +136,7 @@ def parse_args():
 PROFILE_OPS = {"copy", "stream_copy", "reduce", "softmax", "softmax_ragged", "softmax_f16",
                "softmax_f16_ragged", "rmsnorm", "rmsnorm_ragged", "rmsnorm_f16",
                "rmsnorm_f16_ragged", "transpose", "transpose_ragged", "gemm_skinny",
-               "gemm_f32", "gemm_f16", "vendor_gemm_f16", "attention_f16"}
+               "gemm_f32", "gemm_f16", "vendor_gemm_f16", "attention_f16", "attention_f32"}
 # Every HBM-bound kernel, for one counter pass that covers them all.
 BANDWIDTH_OPS = ["copy", "stream_copy", "reduce", "softmax", "softmax_ragged", "softmax_f16",
                  "softmax_f16_ragged", "rmsnorm", "rmsnorm_ragged", "rmsnorm_f16",
@@ -209,6 +209,12 @@ def profile_launchers(torch, lib, ptr, op: str):
         c = torch.empty(n, n, device=dev)
         fn = lib.operatorlib_gemm_f16 if op == "gemm_f16" else lib.operatorlib_gemm_f32
         return [lambda: fn(ptr(a), ptr(b), ptr(c), n, n, n, stream)]
+    if op == "attention_f32":  # B4 H32 S2048 D128, non-causal
+        shape = (4, 32, 2048, 128)
+        q, k, v = (torch.randn(shape, device=dev, generator=gen) for _ in range(3))
+        o = torch.empty(shape, device=dev)
+        return [lambda: lib.operatorlib_attention_f32(ptr(q), ptr(k), ptr(v), ptr(o), 4, 32, 2048,
+                                                      128, 0, stream)]
     # attention_f16, B4 H32 S8192 D128 causal
     shape = (4, 32, 8192, 128)
     q, k, v = (torch.randn(shape, device=dev, generator=gen).half() for _ in range(3))
