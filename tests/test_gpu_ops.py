@@ -751,6 +751,33 @@ def test_attention_f16_reads_no_key_past_the_sequence(lib, heads, s, d, causal):
     assert np.max(np.abs(y[hs, rs] - ref)) <= 2e-3
 
 
+@pytest.mark.parametrize("heads,s,d,causal", POISON_CASES)
+def test_attention_f32_reads_no_key_past_the_sequence(lib, heads, s, d, causal):
+    # The same NaN tail after fp32 Q, K and V, on the fp32 fast-path
+    # instances (the cases span their 64-row, key-split and unsplit grids).
+    q, k, v = _attn_inputs(s, d, False, 1200 + heads + s, heads=heads)
+    tail = 64 * d
+
+    def poisoned(a):
+        flat = torch.full((a.size + tail,), float("nan"), dtype=torch.float32, device="cuda")
+        host = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+        flat[:a.size].copy_(torch.from_numpy(host).to("cuda"))
+        return flat
+
+    dq, dk, dv = (poisoned(a) for a in (q, k, v))
+    out = empty((1, heads, s, d))
+    check(lib.operatorlib_attention_f32(ptr(dq), ptr(dk), ptr(dv), ptr(out), 1, heads, s,
+                                        d, int(causal), stream_handle()), "attention_f32")
+    torch.cuda.synchronize()
+    y = out.cpu().numpy().astype(np.float64).reshape(heads, s, d)
+    assert np.isfinite(y).all()
+    rng = np.random.default_rng(1201)
+    hs = np.concatenate([np.full(s, heads - 1), rng.integers(0, heads, 256)]).astype(np.int32)
+    rs = np.concatenate([np.arange(s), rng.integers(0, s, 256)]).astype(np.int32)
+    ref = oracle.attention(q, k, v, causal, hs, rs)
+    assert np.all(np.abs(y[hs, rs] - ref) <= 1e-4 + 1e-4 * np.abs(ref))
+
+
 def test_attention_pins(hip):
     pins.pin_attention(hip.attention, tol=2e-6)
     f16 = lambda q, k, v, c: hip.attention(*(oracle.to_f16_bits(t) for t in (q, k, v)), c)
