@@ -461,11 +461,13 @@ namespace dma {
 typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// Split of a grid's last, partly filled round: launch indices below
+// Split of a grid's last, partly filled round (or of every tile of a grid
+// too small to fill the CUs, full_tiles = 0): launch indices below
 // full_tiles take whole tiles; the `tiles` tiles after them in the grouped
 // order are each cut into `splits` contiguous K ranges, one workgroup per
-// range, written to `partial` ([splits][tiles][BM x BN] fp32) and summed by
-// sum_tail_kernel. splits == 0: no split, one workgroup per tile.
+// range, written to `partial` ([splits][tiles][BM x BN] fp32, rows past M
+// left unwritten) and summed by sum_tail_kernel. splits == 0: no split,
+// one workgroup per tile.
 struct TailSplit {
   int full_tiles;
   int tiles;
@@ -890,7 +892,8 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
       ? tail.partial + static_cast<std::size_t>(split * tail.tiles + tail_index) * kBM * kBN
       : C + static_cast<std::size_t>(m0) * N + n0;
   const int ldo = split >= 0 ? kBN : N;
-  const int row_end = split >= 0 ? kBM : M - m0;
+  // (a part's rows past M are never summed, so they are not written)
+  const int row_end = min(kBM, M - m0);
   const int col_end = split >= 0 ? kBN : N - n0;
   const bool full = row_end >= kBM && col_end >= kBN;
 #pragma unroll
@@ -1644,16 +1647,11 @@ hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Typ
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const long long blocks =
       tail.splits > 0 ? tail.full_tiles + static_cast<long long>(tail.tiles) * tail.splits : tiles;
-  if constexpr (Cfg::kBM != 256) {  // split tails are for 256 x 256 tiles
-    if (tail.splits > 0) return hipErrorInvalidValue;
-  }
   if (tail.splits > 0) {
-    dma::gemm_dma_kernel<Cfg, Cfg::kBM == 256><<<dim3(static_cast<unsigned>(blocks)),
-                                                 dim3(Cfg::kThreads), 0, stream>>>(
-        a, b, c, m, n, k, ldb, tail);
-    if constexpr (Cfg::kBM == 256)
-      dma::sum_tail_kernel<Cfg><<<dim3(Cfg::kBM * Cfg::kBN / 4 / 256, tail.tiles), dim3(256), 0,
-                                  stream>>>(c, m, n, tail);
+    dma::gemm_dma_kernel<Cfg, true><<<dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads),
+                                      0, stream>>>(a, b, c, m, n, k, ldb, tail);
+    dma::sum_tail_kernel<Cfg><<<dim3(Cfg::kBM * Cfg::kBN / 4 / 256, tail.tiles), dim3(256), 0,
+                                stream>>>(c, m, n, tail);
   } else {
     dma::gemm_dma_kernel<Cfg><<<dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads), 0,
                                 stream>>>(a, b, c, m, n, k, ldb, tail);
@@ -1719,30 +1717,56 @@ struct DmaTiles<float> {
 // Split of the last round of a 256 x 256-tile grid (splits == 0: none).
 struct TailPlan {
   int splits = 0;
-  long long last = 0;  // tiles in the last round
+  long long full = 0;  // tiles computed whole, before the split ones
+  long long last = 0;  // tiles split along K (the last round, or all)
   std::size_t bytes = 0;
 };
 
+// Grids of 128 x 128 tiles (two workgroups per CU) with fewer tiles than
+// CUs split every tile along K instead, into as many parts as fill the
+// workgroup slots (same limits). Small M past the skinny kernels' 16 rows
+// is the case: M = 17..128, N = K = 4096 is 32 tiles. Measured on MI355X
+// (us, whole tiles -> split, B cycling through 8 copies):
+//   fp16 M = 17 30.4 -> 19.7, M = 64 31.8 -> 23.1, M = 128 37.1 -> 29.5,
+//     M = 256 39.4 -> 32.7;
+//   fp32 M = 17 236.8 -> 43.4, M = 64 238.3 -> 46.1, M = 128 237.9 ->
+//     48.0, M = 256 239.4 -> 75.6.
 template <typename T>
 TailPlan tail_plan(int m, int n, int k, std::size_t capacity) {
   TailPlan t;
+  const int cus = device_cus();
+  if (cus <= 0) return t;
   const long long big_tiles =
       static_cast<long long>((m + dma::BigTile::kBM - 1) / dma::BigTile::kBM) *
       ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
-  if (big_tiles < DmaTiles<T>::kSmallBelow) return t;
-  const int cus = device_cus();
-  const long long last = cus > 0 ? big_tiles % cus : 0;
-  if (cus <= 0 || big_tiles <= cus || last == 0 || last > cus / 2) return t;
-  const std::size_t per_split =
-      static_cast<std::size_t>(last) * dma::BigTile::kBM * dma::BigTile::kBN * sizeof(float);
-  long long splits = cus / last;
+  long long split_tiles = 0, full = 0, want = 0;
+  std::size_t tile_bytes = 0;
+  if (big_tiles < DmaTiles<T>::kSmallBelow) {
+    using Small = typename DmaTiles<T>::Small;
+    const long long tiles = static_cast<long long>((m + Small::kBM - 1) / Small::kBM) *
+                            ((n + Small::kBN - 1) / Small::kBN);
+    if (tiles >= cus) return t;
+    split_tiles = tiles;
+    want = 2LL * cus / tiles;
+    tile_bytes = static_cast<std::size_t>(Small::kBM) * Small::kBN * sizeof(float);
+  } else {
+    const long long last = big_tiles % cus;
+    if (big_tiles <= cus || last == 0 || last > cus / 2) return t;
+    split_tiles = last;
+    full = big_tiles - last;
+    want = cus / last;
+    tile_bytes = static_cast<std::size_t>(dma::BigTile::kBM) * dma::BigTile::kBN * sizeof(float);
+  }
+  const std::size_t per_split = static_cast<std::size_t>(split_tiles) * tile_bytes;
+  long long splits = want;
   if (splits > kTailMaxSplits) splits = kTailMaxSplits;
   if (splits > k / kTailMinDepth) splits = k / kTailMinDepth;
   if (static_cast<std::size_t>(splits) > capacity / per_split)
     splits = static_cast<long long>(capacity / per_split);
   if (splits < 2) return t;
   t.splits = static_cast<int>(splits);
-  t.last = last;
+  t.full = full;
+  t.last = split_tiles;
   t.bytes = per_split * static_cast<std::size_t>(splits);
   return t;
 }
@@ -1760,12 +1784,12 @@ hipError_t launch_gemm_dma(const T* a, const T* b, float* c, int m, int n, int k
   const long long big_tiles =
       static_cast<long long>((m + dma::BigTile::kBM - 1) / dma::BigTile::kBM) *
       ((n + dma::BigTile::kBN - 1) / dma::BigTile::kBN);
-  if (big_tiles < Tiles::kSmallBelow)
-    return launch_dma_tiles<typename Tiles::Small>(a, b, c, m, n, k, ldb, stream);
   dma::TailSplit split{0, 0, 0, nullptr};
   if (tail.splits > 0)
-    split = dma::TailSplit{static_cast<int>(big_tiles - tail.last), static_cast<int>(tail.last),
-                           tail.splits, static_cast<float*>(partials)};
+    split = dma::TailSplit{static_cast<int>(tail.full), static_cast<int>(tail.last), tail.splits,
+                           static_cast<float*>(partials)};
+  if (big_tiles < Tiles::kSmallBelow)
+    return launch_dma_tiles<typename Tiles::Small>(a, b, c, m, n, k, ldb, stream, split);
   if (k % Tiles::Big::kBK == 0)
     return launch_dma_tiles<typename Tiles::Big>(a, b, c, m, n, k, ldb, stream, split);
   return launch_dma_tiles<typename Tiles::BigHalfK>(a, b, c, m, n, k, ldb, stream, split);

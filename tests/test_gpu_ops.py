@@ -533,6 +533,29 @@ def test_gemm_f32_step_counts(hip, mnk):
     assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize("mnk", [(17, 4096, 4096), (64, 4096, 4096), (128, 1000, 4096),
+                                 (96, 4100, 2048), (256, 4096, 512), (200, 3000, 2048)])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_gemm_small_m_split_k(hip, mnk, dtype):
+    """M past the skinny kernels' 16 rows on a grid of fewer 128 x 128 tiles
+    than CUs: every tile is split along K (16 parts at K = 4096, 2 at K =
+    512 where the depth limit binds, 10 uneven parts on 48 tiles) and the
+    parts summed; ragged N (1000, 4100), every row checked."""
+    m, n, k = mnk
+    a = oracle.uniform(650 + m, (m, k))
+    b = oracle.uniform(651 + n, (k, n))
+    if dtype == "f16":
+        a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(a, b)
+        ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b))
+        assert np.max(np.abs(y - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b)
+        ref = oracle.gemm(a, b)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
+    assert np.isfinite(y).all()
+
+
 @pytest.mark.parametrize("mnk", [(4097, 4095, 4093), (4352, 4100, 999)])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_gemm_padded_split_tail(hip, mnk, dtype):

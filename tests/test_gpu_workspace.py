@@ -66,12 +66,13 @@ def test_reduce_ws_matches_plain(lib, n):
 # (m, n, k, dtype): narrow decode shapes (split K) on both skinny kernels,
 # padded operands (1000^3, 999 x 1001 x 1003, 4095^3 in both precisions),
 # 272-tile fp16 and fp32 grids whose last round is split, padded operands
-# with a split last round (4097 x 4095 x 4093), shapes that need no scratch.
+# with a split last round (4097 x 4095 x 4093), small-M grids split along K
+# (64 x 4096 x 4096), shapes that need no scratch.
 GEMM_CASES = [(1, 1024, 4096, "f16"), (16, 1024, 4096, "f16"), (1, 1024, 4096, "f32"),
               (16, 1024, 4096, "f32"), (1000, 1000, 1000, "f16"), (4095, 4095, 4095, "f16"),
               (4352, 4096, 512, "f16"), (4352, 4096, 512, "f32"), (1024, 1024, 1024, "f16"),
               (999, 1001, 1003, "f32"), (4095, 4095, 4095, "f32"), (4097, 4095, 4093, "f32"),
-              (500, 500, 999, "f32")]
+              (500, 500, 999, "f32"), (64, 4096, 4096, "f16"), (64, 4096, 4096, "f32")]
 
 
 @pytest.mark.parametrize("m,n,k,dtype", GEMM_CASES)
