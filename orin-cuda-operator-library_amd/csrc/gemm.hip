@@ -7,8 +7,9 @@
 // Reference: operatorlib::gemm_f16 / gemm_f32 (src/gemm.cu:440-479). The
 // reference dispatches between WMMA, cp.async register-tiled and scalar
 // kernels on divisibility; here the dispatch is, in order:
-//   * M <= 16 (decode shapes): the skinny kernels (namespace skinny), an
-//     HBM stream over B with split K and an ordered split sum;
+//   * M <= 16 (decode shapes; the matrix-core one up to 32 fp16 / 64 fp32
+//     rows): the skinny kernels (namespace skinny), an HBM stream over B
+//     with split K and an ordered split sum;
 //   * gemm_dma_kernel (fp16: K % 32 == 0, N % 8 == 0; fp32: K % 16 == 0,
 //     N % 4 == 0; 16-byte aligned operands): direct global->LDS loads,
 //     described before the kernel; 256 x 256 tiles, or 128 x 128 when the
@@ -973,7 +974,7 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4v __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int kMaxM = 16;
+constexpr int kMaxM = 16;  // the vector-ALU kernel's largest M
 constexpr int kLanesPerRow = 16;                     // one 256-byte row segment
 constexpr int kRowGroups = kThreads / kLanesPerRow;  // 16
 constexpr int kWaves = kThreads / opl::kWaveSize;    // 4
@@ -988,6 +989,13 @@ struct Cfg {
   // N = K = 4096: fp16 M 4 -> 11.3 us vector ALU, M 6 -> 12.3 us matrix
   // cores; fp32 M 8 -> 18.7 / 20.6 us, M 12 -> 27.9 / 21.9 us).
   static constexpr int kMfmaMinM = sizeof(T) == 2 ? 5 : 9;
+  // The matrix-core kernel's largest M: 2 row blocks of 16 (fp16) or 4
+  // (fp32). Beyond, the 128 x 128-tile kernel split along K is faster.
+  // Measured on MI355X, N = K = 4096 (us, skinny vs 128 x 128 tiles split
+  // along K): fp16 M = 17 15.7 vs 19.6, M = 32 17.6 vs 20.8, M = 48 25.0
+  // vs 21.9, M = 64 27.5 vs 23.1; fp32 M = 17 23.6 vs 43.3, M = 32 25.0 vs
+  // 44.2, M = 48 41.1 vs 45.1, M = 64 42.1 vs 46.0.
+  static constexpr int kMaxMfmaM = sizeof(T) == 2 ? 32 : 64;
 };
 
 // Row steps (16-byte loads of one or two rows) in flight per thread per
@@ -1170,10 +1178,11 @@ void skinny_kernel(
   }
 }
 
-// Matrix-core variant for larger M (up to 16): one v_mfma_f32_16x16x16_f16
-// (fp16) or v_mfma_f32_16x16x4_f32 (fp32) turns 16 rows of A times a 16 x 16
-// block of B into a 16 x 16 block of C, where the vector-ALU kernel spends
-// one dot product per (m, column pair) and becomes ALU-bound as M grows.
+// Matrix-core variant for larger M (up to 32 fp16, 64 fp32, in row blocks
+// of 16): one v_mfma_f32_16x16x16_f16 (fp16) or v_mfma_f32_16x16x4_f32
+// (fp32) turns 16 rows of A times a 16 x 16 block of B into a 16 x 16 block
+// of C, where the vector-ALU kernel spends one dot product per (m, column
+// pair) and becomes ALU-bound as M grows.
 // B is never transposed: the MFMA only needs A and B to agree on which k
 // fills each of its k slots. K is walked in blocks of 16 rows; lane (g, c)
 // (g = lane / 16, c = lane % 16) owns rows 4g .. 4g+3 of each block (fp32
@@ -1218,7 +1227,9 @@ constexpr int kLaneRows = 4;
 
 // kVecA: K % 4 == 0 and A aligned to 4 elements, so each lane's four A
 // values of a block are one aligned vector, wholly inside or outside k_end.
-template <typename T, bool kVecA>
+// kMB row blocks of 16 (M up to 16 kMB): every B chunk a lane loads feeds
+// one MFMA per row block, so B is still streamed once.
+template <typename T, bool kVecA, int kMB>
 __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
     const T* __restrict__ A, const T* __restrict__ B, float* __restrict__ out,
     int m_rows, int n, int k, int chunk) {
@@ -1229,7 +1240,10 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
   // Rows per lane and k block: 4, or 1 for fp32 without vector A loads.
   constexpr int R = sizeof(T) == 4 && !kVecA ? 1 : kLaneRows;
   constexpr int KB = 4 * R;  // rows per k block
-  constexpr int kBatch = R == 1 ? 16 : MC::kBatch;
+  // k blocks in flight, halved at four row blocks (fp32 only): the full
+  // batch compiled to 193 VGPRs there, one wavefront per SIMD, the half to
+  // 78
+  constexpr int kBatch = (R == 1 ? 16 : MC::kBatch) / (kMB >= 4 ? 2 : 1);
   using AVec = typename std::conditional<R == 1, T, typename MC::AVec>::type;
   // k slot q of a lane's A values
   auto a_at = [](const AVec& a, int q) -> T {
@@ -1247,14 +1261,13 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
   const int c = lane % 16;
   // Columns past N: read a valid chunk (n % P == 0), results not stored.
   const int col = min(n0 + c * P, n - P);
-  const bool a_row = c < m_rows;  // A row c of the MFMA A operand exists
   const int blocks = (k_end - k0 + KB - 1) / KB;
 
   // k block b, lane group g: k rows k0 + KB b + R g + q (q < R). B: a
-  // 16-byte chunk of each row; A: A[c][row] (read from L2, every workgroup
-  // of the split reads the same A). Rows past k_end read valid memory and
-  // are zeroed, as are A rows past m_rows.
-  auto load_block = [&](int b, Vec (&v)[R], AVec& a) {
+  // 16-byte chunk of each row; A: A[16 mb + c][row] of each row block mb
+  // (read from L2, every workgroup of the split reads the same A). Rows
+  // past k_end read valid memory and are zeroed, as are A rows past m_rows.
+  auto load_block = [&](int b, Vec (&v)[R], AVec (&a)[kMB]) {
     const int r0 = k0 + KB * b + R * g;
 #pragma unroll
     for (int q = 0; q < R; ++q) {
@@ -1267,33 +1280,43 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
       v[q] = x;
       if constexpr (!kVecA) {
         // element loads, each issued beside its B row's load
-        const bool a_in = in && a_row;
-        const T av = A[a_in ? static_cast<std::size_t>(c) * k + r : 0];
-        if constexpr (R == 1)
-          a = a_in ? av : T(0);
-        else
-          a[q] = a_in ? av : T(0);
+#pragma unroll
+        for (int mb = 0; mb < kMB; ++mb) {
+          const int arow = 16 * mb + c;
+          const bool a_in = in && arow < m_rows;
+          const T av = A[a_in ? static_cast<std::size_t>(arow) * k + r : 0];
+          if constexpr (R == 1)
+            a[mb] = a_in ? av : T(0);
+          else
+            a[mb][q] = a_in ? av : T(0);
+        }
       }
     }
     if constexpr (kVecA) {
       // r0 % 4 == 0 and k_end % 4 == 0: rows r0 .. r0+3 are all in or all
       // out. Out-of-range lanes read A[0 .. 3] (k >= 4) and zero it.
-      const bool a_in = r0 < k_end && a_row;
-      AVec x = *reinterpret_cast<const AVec*>(
-          A + (a_in ? static_cast<std::size_t>(c) * k + r0 : 0));
 #pragma unroll
-      for (int q = 0; q < R; ++q) a[q] = a_in ? x[q] : T(0);
+      for (int mb = 0; mb < kMB; ++mb) {
+        const int arow = 16 * mb + c;
+        const bool a_in = r0 < k_end && arow < m_rows;
+        AVec x = *reinterpret_cast<const AVec*>(
+            A + (a_in ? static_cast<std::size_t>(arow) * k + r0 : 0));
+#pragma unroll
+        for (int q = 0; q < R; ++q) a[mb][q] = a_in ? x[q] : T(0);
+      }
     }
   };
 
-  floatx4v acc[P];
+  floatx4v acc[kMB][P];
 #pragma unroll
-  for (int j = 0; j < P; ++j)
+  for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[j][e] = 0.0f;
+    for (int j = 0; j < P; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[mb][j][e] = 0.0f;
 
   Vec v[kBatch][R];
-  AVec a[kBatch];
+  AVec a[kBatch][kMB];
   for (int b0 = wave; b0 < blocks; b0 += kWaves * kBatch) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -1309,33 +1332,43 @@ __global__ __launch_bounds__(kThreads) void skinny_mfma_kernel(
             typename MC::AOp bop;
 #pragma unroll
             for (int q = 0; q < R; ++q) bop[q] = v[u][q][j];
-            acc[j] = MC::mma(a[u], bop, acc[j]);
+#pragma unroll
+            for (int mb = 0; mb < kMB; ++mb) acc[mb][j] = MC::mma(a[u][mb], bop, acc[mb][j]);
           } else {
 #pragma unroll
-            for (int q = 0; q < R; ++q) acc[j] = MC::mma(a_at(a[u], q), v[u][q][j], acc[j]);
+            for (int q = 0; q < R; ++q)
+#pragma unroll
+              for (int mb = 0; mb < kMB; ++mb)
+                acc[mb][j] = MC::mma(a_at(a[u][mb], q), v[u][q][j], acc[mb][j]);
           }
         }
       }
     }
   }
 
-  // acc[j][i] = C[4 g + i][n0 + P c + j] of this wavefront's k blocks.
-#pragma unroll
-  for (int j = 0; j < P; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      red[((wave * opl::kWaveSize + lane) * P + j) * 4 + i] = acc[j][i];
-  __syncthreads();
+  // acc[mb][j][i] = C[16 mb + 4 g + i][n0 + P c + j] of this wavefront's
+  // k blocks; the wavefronts' sums go through LDS one row block at a time.
   float* dst = out + static_cast<std::size_t>(blockIdx.y) * m_rows * n;
-  for (int o = tid; o < 16 * BN; o += kThreads) {
-    const int m = o / BN;
-    const int co = o % BN;
-    if (m < m_rows && n0 + co < n) {
-      const int src = ((16 * (m / 4) + co / P) * P + co % P) * 4 + m % 4;
-      float s = red[src];
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) s += red[w * opl::kWaveSize * P * 4 + src];
-      dst[static_cast<std::size_t>(m) * n + n0 + co] = s;
+  for (int mb = 0; mb < kMB; ++mb) {
+    if (mb > 0) __syncthreads();  // the previous block's reads are done
+#pragma unroll
+    for (int j = 0; j < P; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[((wave * opl::kWaveSize + lane) * P + j) * 4 + i] = acc[mb][j][i];
+    __syncthreads();
+    for (int o = tid; o < 16 * BN; o += kThreads) {
+      const int m = o / BN;
+      const int co = o % BN;
+      const int row = 16 * mb + m;
+      if (row < m_rows && n0 + co < n) {
+        const int src = ((16 * (m / 4) + co / P) * P + co % P) * 4 + m % 4;
+        float s = red[src];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) s += red[w * opl::kWaveSize * P * 4 + src];
+        dst[static_cast<std::size_t>(row) * n + n0 + co] = s;
+      }
     }
   }
 }
@@ -1373,9 +1406,20 @@ void launch_m(const T* a, const T* b, float* dst, int m, int n, int k,
   skinny_kernel<T, M><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k, chunk);
 }
 
+template <typename T, int kMB>
+void launch_mfma(bool vec_a, const T* a, const T* b, float* dst, int m, int n, int k,
+                 int chunk, dim3 grid, hipStream_t stream) {
+  if (vec_a)
+    skinny_mfma_kernel<T, true, kMB><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k,
+                                                                        chunk);
+  else
+    skinny_mfma_kernel<T, false, kMB><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k,
+                                                                         chunk);
+}
+
 template <typename T>
 bool applies(const T* b, int m, int n) {
-  return m <= kMaxM && n % Cfg<T>::kPerLane == 0 && opl::aligned16(b);
+  return m <= Cfg<T>::kMaxMfmaM && n % Cfg<T>::kPerLane == 0 && opl::aligned16(b);
 }
 
 // K split of one call: `splits` workgroup rows of `chunk` K rows each (a
@@ -1434,10 +1478,14 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k, const P
     const bool vec_a =
         k % kLaneRows == 0 &&
         reinterpret_cast<std::uintptr_t>(a) % (kLaneRows * sizeof(T)) == 0;
-    if (vec_a)
-      skinny_mfma_kernel<T, true><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k, chunk);
-    else
-      skinny_mfma_kernel<T, false><<<grid, dim3(kThreads), 0, stream>>>(a, b, dst, m, n, k, chunk);
+    if (m <= 16) {
+      launch_mfma<T, 1>(vec_a, a, b, dst, m, n, k, chunk, grid, stream);
+    } else if (m <= 32) {
+      launch_mfma<T, 2>(vec_a, a, b, dst, m, n, k, chunk, grid, stream);
+    } else {
+      if constexpr (C::kMaxMfmaM > 32)
+        launch_mfma<T, 4>(vec_a, a, b, dst, m, n, k, chunk, grid, stream);
+    }
   } else if (m == 1) launch_m<T, 1>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 2) launch_m<T, 2>(a, b, dst, m, n, k, chunk, grid, stream);
   else if (m <= 4) launch_m<T, 4>(a, b, dst, m, n, k, chunk, grid, stream);

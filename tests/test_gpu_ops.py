@@ -356,7 +356,7 @@ def test_gemm_skinny(hip, mnk, dtype):
         assert np.all(np.abs(y - ref) <= 1e-3 + 1e-3 * np.abs(ref))
 
 
-@pytest.mark.parametrize("m", [6, 12, 16])
+@pytest.mark.parametrize("m", [6, 12, 16, 17, 32, 33, 64])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_gemm_skinny_unaligned_a(hip, m, dtype):
     """K % 4 == 0 but A off its 4-element alignment (B aligned, so the
@@ -387,6 +387,34 @@ def test_gemm_skinny_unaligned_a(hip, m, dtype):
 # A loads (offset 1), M 1-16; results deterministic.
 GEMM_DECODE = [(1, 4104, 1000), (7, 3080, 33), (16, 4096, 4095), (2, 4096, 17),
                (16, 6144, 1024), (1, 3072, 1), (11, 12288, 512), (3, 4112, 4100)]
+
+
+# Small batches on the matrix-core skinny kernel: two row blocks of 16
+# (17..32 rows), four (33..64, fp32; fp16 takes the split 128 x 128 tiles
+# there), ragged column blocks (N 4104) and K; misaligned A in
+# test_gemm_skinny_unaligned_a.
+GEMM_SKINNY_ROWS = [(17, 4104, 1000), (24, 4096, 4096), (32, 136, 777), (33, 4104, 1000),
+                    (48, 1000, 333), (64, 4096, 4096)]
+
+
+@pytest.mark.parametrize("mnk", GEMM_SKINNY_ROWS)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_gemm_skinny_row_blocks(hip, mnk, dtype):
+    m, n, k = mnk
+    offset = 0
+    a = oracle.uniform(670 + m, (m, k))
+    b = oracle.uniform(671 + n, (k, n))
+    if dtype == "f16":
+        a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(a, b, offset)
+        ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b))
+        assert np.max(np.abs(y - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b, offset)
+        ref = oracle.gemm(a, b)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
+        assert np.all(np.abs(y - ref) <= 1e-3 + 1e-3 * np.abs(ref))
+    assert np.isfinite(y).all()
 
 
 @pytest.mark.parametrize("mnk", GEMM_DECODE)
@@ -533,14 +561,16 @@ def test_gemm_f32_step_counts(hip, mnk):
     assert np.isfinite(y).all()
 
 
-@pytest.mark.parametrize("mnk", [(17, 4096, 4096), (64, 4096, 4096), (128, 1000, 4096),
-                                 (96, 4100, 2048), (256, 4096, 512), (200, 3000, 2048)])
+@pytest.mark.parametrize("mnk", [(65, 4096, 4096), (100, 4096, 4096), (128, 1000, 4096),
+                                 (96, 4100, 2048), (256, 4096, 512), (200, 3000, 2048),
+                                 (48, 4096, 4096)])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_gemm_small_m_split_k(hip, mnk, dtype):
-    """M past the skinny kernels' 16 rows on a grid of fewer 128 x 128 tiles
-    than CUs: every tile is split along K (16 parts at K = 4096, 2 at K =
-    512 where the depth limit binds, 10 uneven parts on 48 tiles) and the
-    parts summed; ragged N (1000, 4100), every row checked."""
+    """M past the skinny kernels (32 rows fp16, 64 fp32) on a grid of fewer
+    128 x 128 tiles than CUs: every tile is split along K (16 parts at K =
+    4096, 2 at K = 512 where the depth limit binds, 10 uneven parts on 48
+    tiles) and the parts summed; ragged N (1000, 4100); M = 48 fp16. Every
+    row checked."""
     m, n, k = mnk
     a = oracle.uniform(650 + m, (m, k))
     b = oracle.uniform(651 + n, (k, n))
