@@ -10,6 +10,8 @@
 //   * M <= 16 (decode shapes; the matrix-core one up to 32 fp16 / 64 fp32
 //     rows): the skinny kernels (namespace skinny), an HBM stream over B
 //     with split K and an ordered split sum;
+//   * N <= 16 (matrix-vector products): namespace narrow, an HBM stream
+//     over A, one launch;
 //   * gemm_dma_kernel (fp16: K % 32 == 0, N % 8 == 0; fp32: K % 16 == 0,
 //     N % 4 == 0; 16-byte aligned operands): direct global->LDS loads,
 //     described before the kernel; 256 x 256 tiles, or 128 x 128 when the
@@ -1506,6 +1508,141 @@ hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k, const P
 
 }  // namespace skinny
 
+// ---------------------------------------------------------------------------
+// Narrow N (N <= 16: matrix-vector products and a few right-hand columns)
+// for M past the skinny kernels: an HBM stream over A, which the tiled
+// kernels would multiply in 128- or 256-column tiles of mostly padding.
+// Each wavefront owns kRows consecutive rows of A; in every step of K lane
+// l reads 16-byte chunk l of the step's 64 chunks from each of its rows,
+// and the matching E x N block of B (rows k .. k + E - 1, all N columns,
+// contiguous in row-major B: N aligned 16-byte loads, from L2, shared by
+// the wavefront's rows). fp16 multiplies k pairs with v_dot2_f32_f16,
+// fp32 with FMAs, into fp32 partials that are summed over the wavefront
+// in a fixed order at the end. No scratch, one launch.
+// ---------------------------------------------------------------------------
+namespace narrow {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / opl::kWaveSize;
+constexpr int kRows = 4;   // rows of A per wavefront
+constexpr int kMaxN = 16;
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+template <typename T, int N>
+__global__ __launch_bounds__(kThreads) void narrow_kernel(const T* __restrict__ A,
+                                                          const T* __restrict__ B,
+                                                          float* __restrict__ C, int M,
+                                                          int K) {
+  using Vec = typename std::conditional<sizeof(T) == 2, half8, float4v>::type;
+  constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per chunk
+  constexpr int kUnroll = N <= 4 ? 2 : 1;               // K steps in flight
+  const int lane = threadIdx.x % opl::kWaveSize;
+  const int wave = threadIdx.x / opl::kWaveSize;
+  const long long row0 =
+      (static_cast<long long>(blockIdx.x) * kWaves + wave) * kRows;  // wave-uniform
+  if (row0 >= M) return;  // no barrier follows
+  const T* arow[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r)
+    arow[r] = A + static_cast<std::size_t>(min(row0 + r, static_cast<long long>(M) - 1)) * K;
+  float acc[kRows][N];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r)
+#pragma unroll
+    for (int n = 0; n < N; ++n) acc[r][n] = 0.0f;
+
+  const int chunks = K / E;  // K % E == 0
+  for (int c0 = 0; c0 < chunks; c0 += opl::kWaveSize * kUnroll) {
+    Vec a[kUnroll][kRows];
+    Vec b[kUnroll][N];  // b[u][j]: elements E j .. E j + E - 1 of the E x N block
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int c = c0 + opl::kWaveSize * u + lane;
+      const bool in = c < chunks;
+      const int cc = in ? c : 0;
+#pragma unroll
+      for (int r = 0; r < kRows; ++r)
+        a[u][r] = *reinterpret_cast<const Vec*>(arow[r] + static_cast<std::size_t>(cc) * E);
+      const T* bblk = B + static_cast<std::size_t>(cc) * E * N;
+#pragma unroll
+      for (int j = 0; j < N; ++j) b[u][j] = *reinterpret_cast<const Vec*>(bblk + E * j);
+      if (!in) {
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+          for (int e = 0; e < E; ++e) a[u][r][e] = T(0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      // B element (e, n) of the block is b[u][(e N + n) / E][(e N + n) % E].
+      auto belem = [&](int e, int n) -> T {
+        const int i = e * N + n;
+        return b[u][i / E][i % E];
+      };
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int e = 0; e < E; e += 2) {
+#pragma unroll
+          for (int n = 0; n < N; ++n) {
+            half2v bp;
+            bp[0] = belem(e, n);
+            bp[1] = belem(e + 1, n);
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+              half2v ap;
+              ap[0] = a[u][r][e];
+              ap[1] = a[u][r][e + 1];
+              acc[r][n] = __builtin_amdgcn_fdot2(ap, bp, acc[r][n], false);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+#pragma unroll
+          for (int n = 0; n < N; ++n)
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) acc[r][n] = fmaf(a[u][r][e], belem(e, n), acc[r][n]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const float v = opl::wave_reduce<opl::SumOp>(acc[r][n]);
+      if (lane == 0 && row0 + r < M) C[static_cast<std::size_t>(row0 + r) * N + n] = v;
+    }
+  }
+}
+
+template <typename T>
+bool applies(const T* a, const T* b, int n, int k) {
+  constexpr int E = 16 / static_cast<int>(sizeof(T));
+  return n <= kMaxN && k % E == 0 && opl::aligned16(a) && opl::aligned16(b);
+}
+
+template <typename T, int N>
+hipError_t launch_n(const T* a, const T* b, float* c, int m, int k, hipStream_t stream) {
+  const long long rows_per_block = static_cast<long long>(kWaves) * kRows;
+  const long long blocks = (m + rows_per_block - 1) / rows_per_block;
+  narrow_kernel<T, N><<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream>>>(
+      a, b, c, m, k);
+  return hipGetLastError();
+}
+
+template <typename T, int N = 1>
+hipError_t launch(const T* a, const T* b, float* c, int m, int n, int k, hipStream_t stream) {
+  if constexpr (N < kMaxN) {
+    if (n != N) return launch<T, N + 1>(a, b, c, m, n, k, stream);
+  }
+  return launch_n<T, N>(a, b, c, m, k, stream);
+}
+
+}  // namespace narrow
+
 typedef unsigned uint4v __attribute__((ext_vector_type(4)));
 
 // The 16 bytes at p (any 2-byte alignment) from the aligned 16-byte
@@ -1845,7 +1982,7 @@ hipError_t launch_gemm_dma(const T* a, const T* b, float* c, int m, int n, int k
 
 // One call's plan and the scratch it needs.
 struct GemmPlan {
-  enum Kind { kSkinny, kDma, kPaddedDma, kRegister } kind = kRegister;
+  enum Kind { kSkinny, kNarrow, kDma, kPaddedDma, kRegister } kind = kRegister;
   skinny::Plan skinny;
   TailPlan tail;  // kDma, kPaddedDma
   PadPlan pad;    // kPaddedDma
@@ -1863,6 +2000,10 @@ GemmPlan plan_gemm(const T* a, const T* b, int m, int n, int k, std::size_t capa
       p.bytes = p.skinny.bytes;
       return p;
     }
+  }
+  if (narrow::applies(a, b, n, k)) {
+    p.kind = GemmPlan::kNarrow;
+    return p;
   }
   // The copy kernel's per-lane offsets inside a tile are 32-bit: up to
   // 255 rows of A (255 * K * sizeof(T) bytes) and one K step of B rows (64
@@ -1901,6 +2042,8 @@ hipError_t run_gemm(const GemmPlan& p, const T* a, const T* b, float* c, int m, 
   switch (p.kind) {
     case GemmPlan::kSkinny:
       return skinny::launch<T>(a, b, c, m, n, k, p.skinny, scratch, lease, stream);
+    case GemmPlan::kNarrow:
+      return narrow::launch<T>(a, b, c, m, n, k, stream);
     case GemmPlan::kDma:
       return launch_gemm_dma<T>(a, b, c, m, n, k, n, p.tail, scratch, stream);
     case GemmPlan::kPaddedDma: {

@@ -417,6 +417,41 @@ def test_gemm_skinny_row_blocks(hip, mnk, dtype):
     assert np.isfinite(y).all()
 
 
+# Narrow N (<= 16) past the skinny kernels: matrix-vector products and a
+# few right-hand columns on the narrow kernel. Rows past M in the last
+# wavefront, a partial last K step (K = 1000: 125 fp16 / 250 fp32 chunks),
+# K shorter than one step, every N from the instance table's ends, M = 1.
+GEMM_NARROW = [(4096, 1, 4096), (1000, 3, 1000), (517, 16, 2048), (33, 7, 4096),
+               (1, 1, 4096), (2048, 5, 64), (300, 12, 1000), (129, 2, 4096)]
+
+
+@pytest.mark.parametrize("mnk", GEMM_NARROW)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_gemm_narrow_n(hip, mnk, dtype):
+    m, n, k = mnk
+    a = oracle.uniform(676 + m, (m, k))
+    b = oracle.uniform(677 + n, (k, n))
+    if dtype == "f16":
+        a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(a, b)
+        ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b))
+        assert np.max(np.abs(y - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b)
+        ref = oracle.gemm(a, b)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
+        assert np.all(np.abs(y - ref) <= 1e-3 + 1e-3 * np.abs(ref))
+    assert np.isfinite(y).all()
+
+
+def test_gemm_narrow_deterministic(hip):
+    a = oracle.uniform(678, (1000, 4096))
+    b = oracle.uniform(679, (4096, 3))
+    first = hip.gemm_f32(a, b)
+    for _ in range(3):
+        assert np.array_equal(hip.gemm_f32(a, b), first)
+
+
 @pytest.mark.parametrize("mnk", GEMM_DECODE)
 @pytest.mark.parametrize("offset", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
