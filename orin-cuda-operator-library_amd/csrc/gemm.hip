@@ -1713,18 +1713,29 @@ void launch_pad_copy(const T* src, int rows, int cols, T* dst, int rows_p,
 
 inline long long round_up(long long x, long long to) { return (x + to - 1) / to * to; }
 
-// Large GEMMs whose operands miss the direct-to-LDS kernel's rules (K not a
+// GEMMs whose operands miss the direct-to-LDS kernel's rules (K not a
 // multiple of its K step, N not a multiple of one 16-byte chunk, or
-// operands not 16-byte aligned; the 4095^3 edge case) run it on zero-padded
-// aligned copies when the copies fit the call's scratch. Zero rows/columns
-// of K contribute nothing; padded columns of N are never stored. The copies
-// cost a few percent of the product at these sizes; the register-staged
-// kernel on the operands as they are (the fallback when the copies do not
-// fit) costs more: fp16 element-wise 2.5x; fp32 16-byte loads at 4-byte
-// alignment, measured on MI355X (us, in place vs padded): 4095^3 1139 vs
-// 984, 2047^3 234 vs 150, 1100 x 1000 x 999 110 vs 77, 1000^3 78 vs 73.
-inline bool worth_padding(int m, int n, int k) {
-  return m >= 128 && n >= 128 && 2.0 * m * n * static_cast<double>(k) >= 1073741824.0;
+// operands not 16-byte aligned; the 4095^3 edge case) run it on
+// zero-padded aligned copies when the copies fit the call's scratch and
+// the product is not tiny. Zero rows/columns of K contribute nothing;
+// padded columns of N are never stored. The register-staged kernel on the
+// operands as they are (the fallback) loads fp16 odd shapes element by
+// element and runs few, long tiles on small grids, where the padded path
+// splits them along K. Measured on MI355X (us, in place vs padded):
+//   fp16 4096 x 100 x 4096 248 vs 27, 333 x 777 x 999 109 vs 22, 513 x
+//     129 x 1000 90 vs 20, 256 x 255 x 257 39 vs 17, 100^3 17.6 vs 13.8,
+//     50 x 60 x 70 16.3 vs 13.7, but 7 x 37 x 23 10.2 vs 13.6;
+//   fp32 (16-byte loads at 4-byte alignment, no element loads) 4095^3 1139
+//     vs 984, 333 x 777 x 999 100 vs 39, 513 x 129 x 1000 98 vs 36, but
+//     100^3 12.9 vs 18.7, 200^3 20.1 vs 24.4, 256 x 255 x 257 29.8 vs 28.0.
+template <typename T>
+bool worth_padding(int m, int n, int k) {
+  const double flops = 2.0 * m * n * static_cast<double>(k);
+  if (flops >= 134217728.0) return true;  // 2^27
+  if constexpr (sizeof(T) == 2)
+    return flops >= 262144.0;  // 2^18
+  else
+    return k >= 512 && flops >= 16777216.0;  // long K on few tiles (2^24)
 }
 
 // The padded copies of one call: A as [m, kp] and/or B as [kp, np], A's
@@ -2017,7 +2028,7 @@ GemmPlan plan_gemm(const T* a, const T* b, int m, int n, int k, std::size_t capa
     p.bytes = p.tail.bytes;
     return p;
   }
-  if (dma_offsets_fit && worth_padding(m, n, k)) {
+  if (dma_offsets_fit && worth_padding<T>(m, n, k)) {
     const PadPlan pad = pad_plan<T>(a, b, m, n, k, dma::kBK<T>, kChunkElems);
     if (pad.kp <= 0x7fffffffLL && pad.np <= 0x7fffffffLL && pad.bytes() <= capacity) {
       p.kind = GemmPlan::kPaddedDma;

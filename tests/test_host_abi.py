@@ -218,8 +218,10 @@ def test_gemm_workspace_size(lib):
     # 4095^3 fp32: A padded to [4095, 4096], B to [4096, 4096]
     assert f32(FAKE, FAKE, 4095, 4095, 4095) == 4095 * 4096 * 4 + 4096 * 4096 * 4
     assert f32(FAKE, FAKE, 4096, 4096, 4096) == 0  # one whole round of 256 tiles
-    # below 2^30 flop the register-staged kernel reads the operands in place
-    assert f32(FAKE, FAKE, 500, 500, 999) == 0
+    # 500 x 500 x 999 fp32: A padded to [500, 1008], B to [1008, 500]
+    assert f32(FAKE, FAKE, 500, 500, 999) == 500 * 1008 * 4 + 1008 * 500 * 4
+    # small fp32 products with short K read the operands in place
+    assert f32(FAKE, FAKE, 200, 200, 200) == 0
     assert f16(NULL, FAKE, 4095, 4095, 4095) == 0  # invalid arguments
 
 
