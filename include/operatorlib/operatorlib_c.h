@@ -173,8 +173,9 @@ int operatorlib_gemm_f16(const operatorlib_half_t* a,
 
 /*
  * Workspace forms of the GEMMs (see the top of this file): the query gives
- * the scratch bytes of the plan for these operands (padded copies, split
- * partial sums; 0 for most aligned shapes).
+ * the scratch bytes of the plan for these operands (split partial sums,
+ * and padded copies of large fp16 operands whose rows are not 4-byte
+ * aligned; 0 for most shapes).
  * Errors: as the plain forms; a workspace smaller than the query's answer,
  * or NULL or not 256-byte aligned when that is non-zero.
  * No counterpart in the reference (src/gemm.cu:440-479 needs no scratch):

@@ -12,19 +12,19 @@
 //     with split K and an ordered split sum;
 //   * N <= 16 (matrix-vector products): namespace narrow, an HBM stream
 //     over A, one launch;
-//   * gemm_dma_kernel (fp16: K % 32 == 0, N % 8 == 0; fp32: K % 16 == 0,
-//     N % 4 == 0; 16-byte aligned operands): direct global->LDS loads,
-//     described before the kernel; 256 x 256 tiles, or 128 x 128 when the
-//     grid would leave CUs idle;
-//   * large fp16 shapes that miss those rules (e.g. 4095^3): zero-padded
-//     copies of the operands in scratch (the GPU's arena or the caller's
-//     workspace), then the direct-to-LDS kernel (fp32 ones read their rows
-//     in place, below);
-//   * gemm_mfma_kernel, register-staged (Staging below): 16-byte chunks from
-//     16-byte aligned rows (K, N multiples of the chunk, aligned operands),
-//     or 16-byte chunks at 4-byte alignment (every fp32 shape; fp16 with even
-//     K and N), or element-wise with zero fill (any shape and alignment);
-//     fp32 uses 128 x 128 tiles on small grids.
+//   * gemm_dma_kernel (any K, N and alignment, K below 2^22 fp16 / 2^21
+//     fp32 and N below 2^24): direct global->LDS loads that read the
+//     operands in place, described before the kernel; 256 x 256 tiles, or
+//     128 x 128 when the grid would leave CUs idle. Large fp16 products
+//     whose rows are not 4-byte aligned (e.g. 4095^3) first copy those
+//     operands into chunk-padded rows in scratch (the GPU's arena or the
+//     caller's workspace), see PadPlan;
+//   * gemm_mfma_kernel, register-staged (Staging below), for K or N past
+//     those limits: 16-byte chunks from 16-byte aligned rows (K, N
+//     multiples of the chunk, aligned operands), or 16-byte chunks at
+//     4-byte alignment (every fp32 shape; fp16 with even K and N), or
+//     element-wise with zero fill (any shape and alignment); fp32 uses
+//     128 x 128 tiles on small grids.
 // Every path but the vector-ALU skinny kernel (M <= 4 fp16, M <= 8 fp32)
 // runs on the matrix cores.
 //
@@ -436,8 +436,15 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 //     than the deeper prefetch saves;
 //   * copies of steps past the end read through an empty buffer range
 //     (zeros, no memory access), so every step runs the same code;
-//   * M / N edges: source rows / columns are clamped into the matrix (their
-//     results are never stored), stores are masked.
+//   * M / N edges: source rows past M are clamped to M - 1, columns past N
+//     read whatever follows (their results are never stored), stores are
+//     masked; a partly filled last K step is repaired in LDS (fix_stage);
+//   * any row length and alignment: a 16-byte direct-to-LDS copy from any
+//     byte address lands whole, so rows are read in place. Rows at a 2-byte
+//     phase (fp16, odd K or N) cost time, dword-aligned ones nothing (us,
+//     MI355X: fp32 4095^3 925 against 979 on padded copies; fp16 4096 x
+//     4096 x 4095 114 against 128; 1000^3 19 against 32; 100^3 6 against
+//     15).
 // Measured on MI355X (median of 8-launch groups): 4096^3 104-109 us, 8192^3
 // 852-871 us (1.26-1.29 PFLOP/s); hipBLASLt with the same fp32 C: 112-116
 // and 827-859 us. With v_mfma_f32_32x32x16_f16 the same schedule ran
@@ -572,11 +579,11 @@ struct Fragments {
   typename Cfg::Frag b[Cfg::kFN];
 };
 
-template <typename Cfg, bool kTail = false>
+template <typename Cfg, bool kTail = false, bool kEdge = false>
 __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
                      const typename Cfg::Type* __restrict__ B,
-                     float* __restrict__ C, int M, int N, int K, int ldb,
+                     float* __restrict__ C, int M, int N, int K, int lda, int ldb,
                      TailSplit tail) {
   using T = typename Cfg::Type;
   using E = Elem<T>;
@@ -596,7 +603,8 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
   // K steps [kstep0, kstep0 + steps) of the tile; split >= 0: a tail part
   // (kTail instances only; the others keep kstep0 = 0 at compile time).
   int kstep0 = 0;
-  int steps = K / kBK;
+  const int total_steps = (K + kBK - 1) / kBK;
+  int steps = total_steps;
   int split = -1, tail_index = 0;
   if constexpr (kTail) {
     const int b = blockIdx.x;
@@ -630,9 +638,14 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
 
   // DMA sources: copy j of this thread fills LDS chunk slot
   // (wave * kCopies + j) * 64 + lane of each operand tile. They are byte
-  // offsets from the step's scalar bases A + m0 * K + k0 and
-  // B + k0 * ldb + n0 (rows clamped to M - 1, columns to ldb - 8), read
-  // through buffer resources: no 64-bit vector address math per copy.
+  // offsets from the step's scalar bases A + m0 * lda + k0 and
+  // B + k0 * ldb + n0 (A rows clamped to M - 1), read through buffer
+  // resources: no 64-bit vector address math per copy. The copies need no
+  // alignment: a 16-byte copy from any byte address lands whole (measured
+  // on MI355X at every byte phase, at the aligned copy rate), so rows of
+  // any length are read in place. A chunk that runs past its row's end
+  // reads the next row's first elements: past N those fill columns that
+  // are never stored; past K, see fix_stage.
   int a_dma[kCopies];
   int b_dma[kCopies];
 #pragma unroll
@@ -640,10 +653,10 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
     const int slot = (wave * kCopies + j) * 64 + lane;
     const int m = slot / Cfg::kAChunks;
     const int chunk = (slot % Cfg::kAChunks) ^ Cfg::swizzle_a(m);
-    a_dma[j] = (min(m0 + m, M - 1) - m0) * K * kSize + 16 * chunk;
+    a_dma[j] = (min(m0 + m, M - 1) - m0) * lda * kSize + 16 * chunk;
     const int kk = (wave * kCopies + j) * (64 / kBChunks) + lane / kBChunks;
-    const int col = n0 + Cfg::kChunkElems * ((lane % kBChunks) ^ Cfg::swizzle_b(kk));
-    b_dma[j] = kk * ldb * kSize + (min(col, ldb - Cfg::kChunkElems) - n0) * kSize;
+    const int col = Cfg::kChunkElems * ((lane % kBChunks) ^ Cfg::swizzle_b(kk));
+    b_dma[j] = kk * ldb * kSize + col * kSize;
   }
   // Bytes from a step's base to the end of its operand, capped at the
   // 32-bit range (every offset above stays far below it). Steps past the
@@ -652,16 +665,33 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
     return static_cast<unsigned>(bytes < 0xffffffffLL ? bytes : 0xffffffffLL);
   };
   // Operand origins of this tile's first K step (kstep0 > 0: a tail part).
-  const T* const a_tile = A + static_cast<std::size_t>(m0) * K + kstep0 * kBK;
+  const T* const a_tile = A + static_cast<std::size_t>(m0) * lda + kstep0 * kBK;
   const T* const b_tile = B + static_cast<std::size_t>(kstep0) * kBK * ldb + n0;
   const long long a_total =
-      static_cast<long long>(M - m0) * K * kSize - static_cast<long long>(kSize) * kstep0 * kBK;
+      static_cast<long long>(M - m0) * lda * kSize - static_cast<long long>(kSize) * kstep0 * kBK;
   const long long b_total =
       (static_cast<long long>(K) - static_cast<long long>(kstep0) * kBK) * ldb * kSize -
       static_cast<long long>(kSize) * n0;
+  // A last K step that is only partly inside the matrix (K % kBK != 0):
+  // its copies run each A row past column K into the next row's first
+  // elements (B's rows past K lie past B's end and read zeros). The range
+  // check zeroes whole dwords, so with fp16 the dword that holds the last
+  // element of A (odd lda) or of B (odd ldb) together with the first bytes
+  // past the end reads as zero as well. That step runs first (local step 0
+  // copies global step kstep0 + steps - 1, the others follow in order), so
+  // fix_stage repairs it in LDS once, before the K loop: A's columns past K
+  // become zeros and the two end elements are written from copies loaded
+  // at the start. One barrier per tile; the loop itself stays as it is (a
+  // repair inside it cost the fp16 kernel 24 VGPRs and spills).
+  const int k_last = K - (total_steps - 1) * kBK;  // valid k of the last step
+  const bool a_past_k = k_last < kBK;
+  const bool a_end = kSize == 2 && (lda & 1) != 0 && m0 + kBM >= M;
+  const bool b_end = kSize == 2 && (ldb & 1) != 0 && n0 + kBN >= ldb;
+  const bool fix = kEdge && kstep0 + steps == total_steps && (a_past_k || b_end);
+
   auto issue = [&](unsigned char* stage, int kstep) {
-    const int k0 = kstep * kBK;
     const unsigned live = kstep < steps ? ~0u : 0u;
+    const int k0 = (fix ? (kstep == 0 ? steps - 1 : kstep - 1) : kstep) * kBK;
     const unsigned a_span = span(a_total - static_cast<long long>(kSize) * k0) & live;
     const unsigned b_span = span(b_total - static_cast<long long>(kSize) * k0 * ldb) & live;
     const T* a_base = a_tile + k0;
@@ -673,6 +703,46 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
       opl::buffer_copy16_lds(b_base, b_span, stage + kABytes + (wave * kCopies + j) * 1024,
                              b_dma[j]);
     }
+  };
+
+  __shared__ T end_elems[2];
+  T a_end_value = T(0), b_end_value = T(0);
+  if (fix && threadIdx.x == 0) {
+    if (a_end) a_end_value = A[static_cast<std::size_t>(M) * lda - 1];
+    if (b_end) b_end_value = B[static_cast<std::size_t>(K) * ldb - 1];
+  }
+  // Called on stage 0 after the first barrier.
+  auto fix_stage = [&](unsigned char* st) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int E = Cfg::kChunkElems;
+    OPL_LDS unsigned char* const s = (OPL_LDS unsigned char*)st;
+    const int tid = threadIdx.x;
+    if (a_past_k) {
+      for (int m = tid; m < kBM; m += Cfg::kThreads) {
+        OPL_LDS unsigned char* const row = s + m * Cfg::kARowBytes;
+        const int sw = Cfg::swizzle_a(m);
+        if (k_last % E != 0) {  // the chunk across column K, element by element
+          OPL_LDS T* const c = (OPL_LDS T*)(row + (((k_last / E) ^ sw) * 16));
+          for (int e = k_last % E; e < E; ++e) c[e] = T(0);
+        }
+        for (int c = (k_last + E - 1) / E; c < Cfg::kAChunks; ++c)
+          *(OPL_LDS u32x4*)(row + ((c ^ sw) * 16)) = u32x4{0u, 0u, 0u, 0u};
+      }
+      if (a_end && tid == 0) {
+        const int m = M - 1 - m0, kk = k_last - 1;
+        ((OPL_LDS T*)(s + m * Cfg::kARowBytes + (((kk / E) ^ Cfg::swizzle_a(m)) * 16)))[kk % E] =
+            end_elems[0];
+      }
+    }
+    if (b_end && tid == 0) {
+      const int kk = k_last - 1, n = ldb - 1 - n0;
+      ((OPL_LDS T*)(s + kABytes + kk * Cfg::kBRowBytes +
+                    (((n / E) ^ Cfg::swizzle_b(kk)) * 16)))[n % E] = end_elems[1];
+    }
+    // s_waitcnt lgkmcnt(0), copies left in flight; then every wave's writes
+    // are in place
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("s_barrier" ::: "memory");
   };
 
   // Fragment byte offsets inside a stage (lane l supplies row / column
@@ -838,8 +908,13 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
     };
     issue(stage0, 0);
     issue(stage1, 1);
+    if (fix && threadIdx.x == 0) {
+      end_elems[0] = a_end_value;
+      end_elems[1] = b_end_value;
+    }
     wait_copies(std::integral_constant<int, kIssues>());
     asm volatile("s_barrier" ::: "memory");
+    if (fix) fix_stage(stage0);
     load(stage0, 0, f0);
     __builtin_amdgcn_sched_barrier(0);
     int step = 0;
@@ -872,8 +947,13 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
     issue(stage1, 1);
     issue(stage2, 2);
     issue(stage3, 3);
+    if (fix && threadIdx.x == 0) {
+      end_elems[0] = a_end_value;
+      end_elems[1] = b_end_value;
+    }
     wait_copies(std::integral_constant<int, 3 * kIssues>());
     asm volatile("s_barrier" ::: "memory");
+    if (fix) fix_stage(stage0);
     load(stage0, 0, f0);
     __builtin_amdgcn_sched_barrier(0);
     int step = 0;
@@ -1668,121 +1748,102 @@ __device__ __forceinline__ uint4v load16_shifted(const void* p) {
   return out;
 }
 
-// Copies a row-major [rows, cols] matrix into a zero-padded row-major
-// [rows_p, cols_p] one (cols_p a multiple of one 16-byte chunk, 16-byte
-// aligned destination): each thread writes whole chunks. A chunk whose
-// source elements all exist is read as 16 bytes from the aligned chunk(s)
-// covering it (rows of an odd-width fp16 matrix start at any 2-byte
-// phase); the last chunk of a row and the padding rows go element by
-// element.
-template <typename T>
-__global__ __launch_bounds__(256) void pad_copy_kernel(
-    const T* __restrict__ src, int rows, int cols, T* __restrict__ dst,
-    int rows_p, int cols_p) {
-  using Chunk = typename Precision<T>::Chunk;
-  constexpr int E = Precision<T>::kChunkElems;
+// Copies a row-major fp16 [rows, cols] matrix into a zero-padded row-major
+// [rows_p, cols_p] one whose rows are whole 16-byte chunks (cols_p a
+// multiple of 8, 16-byte aligned destination): each thread writes whole
+// chunks. A chunk whose source elements all exist is read as 16 bytes from
+// the aligned chunk(s) covering it (the rows of an odd-width matrix start
+// at every 2-byte phase); a row's last chunk and the padding rows go
+// element by element.
+__global__ __launch_bounds__(256) void pad_copy_kernel(const _Float16* __restrict__ src,
+                                                       int rows, int cols,
+                                                       _Float16* __restrict__ dst,
+                                                       int rows_p, int cols_p) {
+  using Chunk = Precision<_Float16>::Chunk;
+  constexpr int E = Precision<_Float16>::kChunkElems;
   const long long per_row = cols_p / E;
   const long long total = static_cast<long long>(rows_p) * per_row;
   for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
        i < total; i += static_cast<long long>(gridDim.x) * blockDim.x) {
     const int r = static_cast<int>(i / per_row);
     const int c0 = static_cast<int>(i % per_row) * E;
-    const T* s = src + static_cast<std::size_t>(r) * cols;
+    const _Float16* s = src + static_cast<std::size_t>(r) * cols;
     Chunk v;
     if (r < rows && c0 + E <= cols) {
       v = __builtin_bit_cast(Chunk, load16_shifted(s + c0));
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e)
-        v[e] = (r < rows && c0 + e < cols) ? s[c0 + e] : T(0);
+        v[e] = (r < rows && c0 + e < cols) ? s[c0 + e] : _Float16(0);
     }
     *reinterpret_cast<Chunk*>(dst + static_cast<std::size_t>(r) * cols_p + c0) = v;
   }
 }
 
-template <typename T>
-void launch_pad_copy(const T* src, int rows, int cols, T* dst, int rows_p,
+void launch_pad_copy(const _Float16* src, int rows, int cols, _Float16* dst, int rows_p,
                      int cols_p, hipStream_t stream) {
-  constexpr int E = Precision<T>::kChunkElems;
-  const long long chunks = static_cast<long long>(rows_p) * (cols_p / E);
+  const long long chunks = static_cast<long long>(rows_p) * (cols_p / 8);
   const long long blocks = (chunks + 255) / 256;
-  pad_copy_kernel<T><<<dim3(static_cast<unsigned>(blocks < 8192 ? blocks : 8192)),
-                       dim3(256), 0, stream>>>(src, rows, cols, dst, rows_p,
-                                               cols_p);
+  pad_copy_kernel<<<dim3(static_cast<unsigned>(blocks < 8192 ? blocks : 8192)), dim3(256), 0,
+                    stream>>>(src, rows, cols, dst, rows_p, cols_p);
 }
 
 inline long long round_up(long long x, long long to) { return (x + to - 1) / to * to; }
 
-// GEMMs whose operands miss the direct-to-LDS kernel's rules (K not a
-// multiple of its K step, N not a multiple of one 16-byte chunk, or
-// operands not 16-byte aligned; the 4095^3 edge case) run it on
-// zero-padded aligned copies when the copies fit the call's scratch and
-// the product is not tiny. Zero rows/columns of K contribute nothing;
-// padded columns of N are never stored. The register-staged kernel on the
-// operands as they are (the fallback) loads fp16 odd shapes element by
-// element and runs few, long tiles on small grids, where the padded path
-// splits them along K. Measured on MI355X (us, in place vs padded):
-//   fp16 4096 x 100 x 4096 248 vs 27, 333 x 777 x 999 109 vs 22, 513 x
-//     129 x 1000 90 vs 20, 256 x 255 x 257 39 vs 17, 100^3 17.6 vs 13.8,
-//     50 x 60 x 70 16.3 vs 13.7, but 7 x 37 x 23 10.2 vs 13.6;
-//   fp32 (16-byte loads at 4-byte alignment, no element loads) 4095^3 1139
-//     vs 984, 333 x 777 x 999 100 vs 39, 513 x 129 x 1000 98 vs 36, but
-//     100^3 12.9 vs 18.7, 200^3 20.1 vs 24.4, 256 x 255 x 257 29.8 vs 28.0.
-template <typename T>
-bool worth_padding(int m, int n, int k) {
-  const double flops = 2.0 * m * n * static_cast<double>(k);
-  if (flops >= 134217728.0) return true;  // 2^27
-  if constexpr (sizeof(T) == 2)
-    return flops >= 262144.0;  // 2^18
-  else
-    return k >= 512 && flops >= 16777216.0;  // long K on few tiles (2^24)
-}
-
-// The padded copies of one call: A as [m, kp] and/or B as [kp, np], A's
-// copy first in scratch, B's at a 256-byte boundary after it.
+// The direct-to-LDS kernel reads every operand in place, but fp16 rows
+// that are not 4-byte aligned (odd K for A, odd N for B, or a base off a
+// 4-byte boundary) start their 16-byte copies at a 2-byte phase, and those
+// copies cost it time; dword-aligned rows cost nothing. Measured on MI355X
+// (us, kernel alone): 4095^3 132 against 107 for the same grid aligned,
+// 4097 x 4095 x 4093 150 against 119; 4096^3 with every row of A and B at
+// a 2-byte phase 155 against 113, A only 126, B only 123; odd K only 119,
+// odd N only 113; 8192 x 8191 x 8191 1106 against 871, odd K only 1046,
+// odd N only 968. Dword-aligned: fp16 K = 4094 111, fp32 4095^3 928
+// against 926. Large products therefore first copy such operands into
+// rows padded to a whole number of chunks (about 11.5 us per 4095^2
+// operand): both when both are off (from 10^11 flop, about 3700^3), one
+// alone from 2.75 * 10^11 (about 5200^3). One operand alone is copied with
+// its rows padded to a whole number of chunks (A [M, round_up(K, 8)], B
+// [K, round_up(N, 8)]) and the kernel repairs K's last step itself. Both
+// are also padded along K to a multiple of 64 (A [M, K'], B [K', N'],
+// zeros past K): the kernel then runs its plain schedule.
 struct PadPlan {
   bool pad_a = false, pad_b = false;
-  long long kp = 0, np = 0;
-  std::size_t a_bytes = 0, b_bytes = 0;
+  int k = 0;             // the K the kernel runs with
+  int lda = 0, ldb = 0;  // row strides it reads with
+  std::size_t a_bytes = 0, b_bytes = 0;  // each rounded to 256 bytes
   std::size_t bytes() const { return a_bytes + b_bytes; }
 };
 
 template <typename T>
-PadPlan pad_plan(const T* a, const T* b, int m, int n, int k, int k_mult, int n_mult) {
+PadPlan pad_plan(const T* a, const T* b, int m, int n, int k) {
   PadPlan p;
-  p.kp = round_up(k, k_mult);
-  p.np = round_up(n, n_mult);
-  p.pad_a = p.kp != k || !opl::aligned16(a);
-  p.pad_b = p.kp != k || p.np != n || !opl::aligned16(b);
-  if (p.pad_a)
-    p.a_bytes = static_cast<std::size_t>(round_up(static_cast<long long>(m) * p.kp * sizeof(T), 256));
-  if (p.pad_b)
-    p.b_bytes = static_cast<std::size_t>(round_up(p.kp * p.np * static_cast<long long>(sizeof(T)), 256));
+  p.k = k;
+  p.lda = k;
+  p.ldb = n;
+  if constexpr (sizeof(T) == 2) {
+    auto dword = [](const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 3u) == 0; };
+    const bool off_a = k % 2 != 0 || !dword(a);
+    const bool off_b = n % 2 != 0 || !dword(b);
+    const double flops = 2.0 * m * n * static_cast<double>(k);
+    const double from = off_a && off_b ? 1.0e11 : 2.75e11;
+    if ((!off_a && !off_b) || flops < from) return p;
+    const long long kk = off_a && off_b ? round_up(k, 64) : k;  // K the kernel runs with
+    const long long kp = round_up(kk, 8), np = round_up(n, 8);
+    if (kp > 0x7fffffffLL || np > 0x7fffffffLL) return p;
+    p.pad_a = off_a;
+    p.pad_b = off_b;
+    p.k = static_cast<int>(kk);
+    if (p.pad_a) {
+      p.lda = static_cast<int>(kp);
+      p.a_bytes = static_cast<std::size_t>(round_up(static_cast<long long>(m) * kp * 2, 256));
+    }
+    if (p.pad_b) {
+      p.ldb = static_cast<int>(np);
+      p.b_bytes = static_cast<std::size_t>(round_up(kk * np * 2, 256));
+    }
+  }
   return p;
-}
-
-struct PaddedOperands {
-  const void* a;
-  const void* b;
-  int k;    // padded K (row stride of A)
-  int ldb;  // row stride of B
-};
-
-// Enqueues the copies of plan `pp` into `ws` (pp.bytes() of scratch).
-template <typename T>
-PaddedOperands pad_into(const T* a, const T* b, int m, int n, int k, const PadPlan& pp,
-                        void* ws, hipStream_t stream) {
-  T* pa = static_cast<T*>(ws);
-  T* pb = reinterpret_cast<T*>(static_cast<unsigned char*>(ws) + pp.a_bytes);
-  if (pp.pad_a) launch_pad_copy<T>(a, m, k, pa, m, static_cast<int>(pp.kp), stream);
-  if (pp.pad_b)
-    launch_pad_copy<T>(b, k, n, pb, static_cast<int>(pp.kp), static_cast<int>(pp.np), stream);
-  PaddedOperands out;
-  out.a = pp.pad_a ? static_cast<const void*>(pa) : a;
-  out.b = pp.pad_b ? static_cast<const void*>(pb) : b;
-  out.k = static_cast<int>(pp.kp);
-  out.ldb = pp.pad_b ? static_cast<int>(pp.np) : n;
-  return out;
 }
 
 // One launch of gemm_mfma_kernel with tile layout L and staging `staging`.
@@ -1836,21 +1897,32 @@ int staging_for(const T* a, const T* b, int n, int k) {
 
 template <typename Cfg>
 hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Type* b, float* c,
-                            int m, int n, int k, int ldb, hipStream_t stream,
+                            int m, int n, int k, int lda, int ldb, hipStream_t stream,
                             dma::TailSplit tail = {0, 0, 0, nullptr}) {
   const long long tiles = static_cast<long long>((m + Cfg::kBM - 1) / Cfg::kBM) *
                           ((n + Cfg::kBN - 1) / Cfg::kBN);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const long long blocks =
       tail.splits > 0 ? tail.full_tiles + static_cast<long long>(tail.tiles) * tail.splits : tiles;
+  // Shapes with a partly filled last K step, or fp16 rows of odd length,
+  // run the instance that repairs that step (the others keep the plain
+  // schedule: the repair's code cost the aligned 4096^3 product 2%).
+  const bool edge = k % Cfg::kBK != 0 || (sizeof(typename Cfg::Type) == 2 && (lda % 2 != 0 || ldb % 2 != 0));
+  const dim3 grid(static_cast<unsigned>(blocks)), block(Cfg::kThreads);
   if (tail.splits > 0) {
-    dma::gemm_dma_kernel<Cfg, true><<<dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads),
-                                      0, stream>>>(a, b, c, m, n, k, ldb, tail);
+    if (edge)
+      dma::gemm_dma_kernel<Cfg, true, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k, lda,
+                                                                        ldb, tail);
+    else
+      dma::gemm_dma_kernel<Cfg, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k, lda, ldb,
+                                                                  tail);
     dma::sum_tail_kernel<Cfg><<<dim3(Cfg::kBM * Cfg::kBN / 4 / 256, tail.tiles), dim3(256), 0,
                                 stream>>>(c, m, n, tail);
+  } else if (edge) {
+    dma::gemm_dma_kernel<Cfg, false, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k, lda,
+                                                                       ldb, tail);
   } else {
-    dma::gemm_dma_kernel<Cfg><<<dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads), 0,
-                                stream>>>(a, b, c, m, n, k, ldb, tail);
+    dma::gemm_dma_kernel<Cfg><<<grid, block, 0, stream>>>(a, b, c, m, n, k, lda, ldb, tail);
   }
   return hipGetLastError();
 }
@@ -1967,10 +2039,10 @@ TailPlan tail_plan(int m, int n, int k, std::size_t capacity) {
   return t;
 }
 
-// The direct-to-LDS kernel (k % dma::kBK<T> == 0) on 128 x 128 or 256 x 256
+// The direct-to-LDS kernel (any K, N and alignment) on 128 x 128 or 256 x 256
 // tiles, with `tail` split into `partials` (tail.bytes of scratch).
 template <typename T>
-hipError_t launch_gemm_dma(const T* a, const T* b, float* c, int m, int n, int k, int ldb,
+hipError_t launch_gemm_dma(const T* a, const T* b, float* c, int m, int n, int k, int lda, int ldb,
                            const TailPlan& tail, void* partials, hipStream_t stream) {
   using Tiles = DmaTiles<T>;
   static_assert(Tiles::Big::kBM == dma::BigTile::kBM && Tiles::Big::kBN == dma::BigTile::kBN &&
@@ -1985,18 +2057,20 @@ hipError_t launch_gemm_dma(const T* a, const T* b, float* c, int m, int n, int k
     split = dma::TailSplit{static_cast<int>(tail.full), static_cast<int>(tail.last), tail.splits,
                            static_cast<float*>(partials)};
   if (big_tiles < Tiles::kSmallBelow)
-    return launch_dma_tiles<typename Tiles::Small>(a, b, c, m, n, k, ldb, stream, split);
-  if (k % Tiles::Big::kBK == 0)
-    return launch_dma_tiles<typename Tiles::Big>(a, b, c, m, n, k, ldb, stream, split);
-  return launch_dma_tiles<typename Tiles::BigHalfK>(a, b, c, m, n, k, ldb, stream, split);
+    return launch_dma_tiles<typename Tiles::Small>(a, b, c, m, n, k, lda, ldb, stream, split);
+  // A last step at most half full runs on the half-deep stages.
+  const int rest = k % Tiles::Big::kBK;
+  if (rest == 0 || rest > Tiles::BigHalfK::kBK)
+    return launch_dma_tiles<typename Tiles::Big>(a, b, c, m, n, k, lda, ldb, stream, split);
+  return launch_dma_tiles<typename Tiles::BigHalfK>(a, b, c, m, n, k, lda, ldb, stream, split);
 }
 
 // One call's plan and the scratch it needs.
 struct GemmPlan {
-  enum Kind { kSkinny, kNarrow, kDma, kPaddedDma, kRegister } kind = kRegister;
+  enum Kind { kSkinny, kNarrow, kDma, kRegister } kind = kRegister;
   skinny::Plan skinny;
-  TailPlan tail;  // kDma, kPaddedDma
-  PadPlan pad;    // kPaddedDma
+  TailPlan tail;  // kDma
+  PadPlan pad;    // kDma
   int staging = kElementwise;  // kRegister
   std::size_t bytes = 0;
 };
@@ -2020,25 +2094,15 @@ GemmPlan plan_gemm(const T* a, const T* b, int m, int n, int k, std::size_t capa
   // 255 rows of A (255 * K * sizeof(T) bytes) and one K step of B rows (64
   // fp16 or 32 fp32 rows: 128 * N bytes).
   const bool dma_offsets_fit = k < (sizeof(T) == 2 ? (1 << 22) : (1 << 21)) && n < (1 << 24);
-  constexpr int kChunkElems = 16 / static_cast<int>(sizeof(T));
-  if (dma_offsets_fit && k % dma::kBK<T> == 0 && n % kChunkElems == 0 && opl::aligned16(a) &&
-      opl::aligned16(b)) {
+  if (dma_offsets_fit) {
     p.kind = GemmPlan::kDma;
-    p.tail = tail_plan<T>(m, n, k, capacity);
-    p.bytes = p.tail.bytes;
+    p.pad = pad_plan<T>(a, b, m, n, k);
+    if (p.pad.bytes() > capacity) p.pad = PadPlan{false, false, k, k, n, 0, 0};
+    // The split partials of a partly filled last round follow the copies,
+    // in what is left of the capacity.
+    p.tail = tail_plan<T>(m, n, p.pad.k, capacity - p.pad.bytes());
+    p.bytes = p.pad.bytes() + p.tail.bytes;
     return p;
-  }
-  if (dma_offsets_fit && worth_padding<T>(m, n, k)) {
-    const PadPlan pad = pad_plan<T>(a, b, m, n, k, dma::kBK<T>, kChunkElems);
-    if (pad.kp <= 0x7fffffffLL && pad.np <= 0x7fffffffLL && pad.bytes() <= capacity) {
-      p.kind = GemmPlan::kPaddedDma;
-      p.pad = pad;
-      // The split partials of a partly filled last round follow the copies,
-      // in what is left of the capacity.
-      p.tail = tail_plan<T>(m, n, static_cast<int>(pad.kp), capacity - pad.bytes());
-      p.bytes = pad.bytes() + p.tail.bytes;
-      return p;
-    }
   }
   p.kind = GemmPlan::kRegister;
   p.staging = staging_for<T>(a, b, n, k);
@@ -2055,14 +2119,25 @@ hipError_t run_gemm(const GemmPlan& p, const T* a, const T* b, float* c, int m, 
       return skinny::launch<T>(a, b, c, m, n, k, p.skinny, scratch, lease, stream);
     case GemmPlan::kNarrow:
       return narrow::launch<T>(a, b, c, m, n, k, stream);
-    case GemmPlan::kDma:
-      return launch_gemm_dma<T>(a, b, c, m, n, k, n, p.tail, scratch, stream);
-    case GemmPlan::kPaddedDma: {
-      // Both copies' sizes are rounded to 256 bytes: the partials start aligned.
-      const PaddedOperands q = pad_into<T>(a, b, m, n, k, p.pad, scratch, stream);
-      void* const partials = static_cast<unsigned char*>(scratch) + p.pad.bytes();
-      return launch_gemm_dma<T>(static_cast<const T*>(q.a), static_cast<const T*>(q.b), c, m, n,
-                                q.k, q.ldb, p.tail, partials, stream);
+    case GemmPlan::kDma: {
+      const T* pa = a;
+      const T* pb = b;
+      unsigned char* const ws = static_cast<unsigned char*>(scratch);
+      if constexpr (sizeof(T) == 2) {
+        // Both copies' sizes are rounded to 256 bytes: the partials start aligned.
+        if (p.pad.pad_a) {
+          launch_pad_copy(a, m, k, reinterpret_cast<T*>(ws), m, p.pad.lda, stream);
+          pa = reinterpret_cast<const T*>(ws);
+        }
+        if (p.pad.pad_b) {
+          launch_pad_copy(b, k, n, reinterpret_cast<T*>(ws + p.pad.a_bytes), p.pad.k,
+                          p.pad.ldb, stream);
+          pb = reinterpret_cast<const T*>(ws + p.pad.a_bytes);
+        }
+      }
+      void* const partials = ws != nullptr ? ws + p.pad.bytes() : nullptr;
+      return launch_gemm_dma<T>(pa, pb, c, m, n, p.pad.k, p.pad.lda, p.pad.ldb, p.tail,
+                                partials, stream);
     }
     default:
       return launch_generic_for<T>(p.staging, a, b, c, m, n, k, n, stream);

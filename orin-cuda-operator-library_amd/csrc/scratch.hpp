@@ -8,10 +8,11 @@
 // means fewer splits or a slower kernel, never an error):
 //   * reduce: one fp64 partial per workgroup (at most 2 KiB);
 //   * decode GEMMs (M <= 16): split-K partial sums;
-//   * fp16 GEMMs whose operands miss the direct-to-LDS kernel's shape or
-//     alignment rules: zero-padded operand copies;
-//   * fp16 GEMMs whose last round of 256 x 256 tiles fills at most half the
-//     CUs: split-K partial tiles of that round;
+//   * large fp16 GEMMs whose rows are not 4-byte aligned: operand copies
+//     with chunk-padded rows;
+//   * GEMMs whose last round of 256 x 256 tiles fills at most half the CUs,
+//     or whose grid of 128 x 128 tiles is smaller than the CU count:
+//     split-K partial tiles;
 //   * register-staged attention on small grids: per-split partials.
 // The reference launchers need none of this (src/reduce.cu:54-69 combines
 // with float atomics after an in-stream memset) and are reentrant because
@@ -50,9 +51,9 @@
 namespace opl {
 
 // Bytes of each GPU's arena (under 0.1% of an MI355X's 288 GB). It holds
-// the padded operands of GEMMs up to 5120 x 5120 x 5120 in fp32 (200 MiB)
-// or 7168^3 in fp16, and every plan at the reference's benchmark sizes in
-// full, split last rounds included.
+// the padded copies of fp16 GEMM operands up to 8191^3 (both copied, 256
+// MiB), and every plan at the reference's benchmark sizes in full, split
+// last rounds included.
 constexpr std::size_t kArenaBytes = std::size_t(256) << 20;
 
 // Plans are computed for a scratch capacity: kUnlimited for workspace-size

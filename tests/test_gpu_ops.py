@@ -496,15 +496,16 @@ def test_gemm_skinny_deterministic(hip):
         assert np.array_equal(hip.gemm_f16(ah, bh), first)
 
 
-# Large shapes that miss the fast kernels' rules and run on zero-padded
-# copies of A and/or B (K or N off the chunk multiple, or unaligned).
-GEMM_PADDED = [(1000, 1000, 1000), (1024, 1030, 1024), (1100, 1000, 999), (640, 768, 1800)]
+# Shapes whose rows are not whole 16-byte chunks or K steps (K or N off the
+# chunk multiple, or an unaligned base): the direct-to-LDS kernel reads
+# them in place.
+GEMM_UNALIGNED = [(1000, 1000, 1000), (1024, 1030, 1024), (1100, 1000, 999), (640, 768, 1800)]
 
 
-@pytest.mark.parametrize("mnk", GEMM_PADDED)
+@pytest.mark.parametrize("mnk", GEMM_UNALIGNED)
 @pytest.mark.parametrize("offset", [0, 1])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_gemm_padded_operands(hip, mnk, offset, dtype):
+def test_gemm_unaligned_operands(hip, mnk, offset, dtype):
     m, n, k = mnk
     a = oracle.uniform(620 + m, (m, k))
     b = oracle.uniform(621 + n, (k, n))
@@ -623,10 +624,10 @@ def test_gemm_small_m_split_k(hip, mnk, dtype):
 
 @pytest.mark.parametrize("mnk", [(4097, 4095, 4093), (4352, 4100, 999)])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
-def test_gemm_padded_split_tail(hip, mnk, dtype):
-    """Padded operands on a grid one round plus 16 (33) 256 x 256 tiles
-    long: the last round is split along K (16 parts; 3 parts) into partials
-    placed after the padded copies in the same scratch."""
+def test_gemm_unaligned_split_tail(hip, mnk, dtype):
+    """Unaligned operands on a grid one round plus 16 (33) 256 x 256 tiles
+    long: the last round is split along K (16 parts; 3 parts), and the
+    last part repairs the partly filled last K step."""
     m, n, k = mnk
     a = oracle.uniform(640 + m, (m, k))
     b = oracle.uniform(641 + n, (k, n))
@@ -643,9 +644,9 @@ def test_gemm_padded_split_tail(hip, mnk, dtype):
     assert np.isfinite(y).all()
 
 
-def test_gemm_padded_then_smaller(hip):
-    """The arena is reused: a large padded call followed by a smaller one
-    and a larger one must all be right."""
+def test_gemm_split_then_smaller(hip):
+    """The arena is reused: a call with split partials followed by a smaller
+    one and a larger one must all be right."""
     for m, n, k in [(1200, 1100, 1001), (700, 800, 1999), (1500, 1500, 1500)]:
         a = oracle.uniform(630 + m, (m, k))
         b = oracle.uniform(631 + n, (k, n))
@@ -654,6 +655,123 @@ def test_gemm_padded_then_smaller(hip):
         rows = np.array([0, 1, m // 2, m - 2, m - 1])
         ref = oracle.gemm(oracle.from_f16_bits(ab), oracle.from_f16_bits(bb), rows)
         assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+
+
+# Shapes off every rule of the skinny and narrow kernels (odd N, odd K),
+# K shorter than one K step, single rows and columns: all run the
+# direct-to-LDS kernel in place, whose first step is the partly filled
+# last one.
+GEMM_ODD = [(1, 1001, 333), (3, 7, 5), (17, 9, 1), (100, 5, 33), (129, 257, 63),
+            (300, 301, 7), (65, 1000, 4095), (257, 255, 97)]
+
+
+@pytest.mark.parametrize("mnk", GEMM_ODD)
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_gemm_odd_shapes(hip, mnk, offset, dtype):
+    m, n, k = mnk
+    a = oracle.uniform(690 + m, (m, k))
+    b = oracle.uniform(691 + n, (k, n))
+    if dtype == "f16":
+        ab, bb = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(ab, bb, offset)
+        ref = oracle.gemm(oracle.from_f16_bits(ab), oracle.from_f16_bits(bb))
+        assert np.max(np.abs(y - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b, offset)
+        ref = oracle.gemm(a, b)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) <= 1e-4
+        assert np.all(np.abs(y - ref) <= 1e-3 + 1e-3 * np.abs(ref))
+
+
+# Grids of 256 x 256 tiles whose last K step is partly filled, on both the
+# 64-deep (fp32: 32) and the half-deep stages, with odd N; and medium grids.
+GEMM_PARTIAL_STEP = [(4096, 4095, 3999), (4096, 4095, 4001), (4095, 4097, 3983),
+                     (2000, 1999, 1001)]
+
+
+@pytest.mark.parametrize("mnk", GEMM_PARTIAL_STEP)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_gemm_partial_last_step(hip, mnk, dtype):
+    m, n, k = mnk
+    a = oracle.uniform(700 + k, (m, k))
+    b = oracle.uniform(701 + n, (k, n))
+    rows = tile_row_rows(m, 702)
+    if dtype == "f16":
+        a, b = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        y = hip.gemm_f16(a, b)
+        ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b), rows)
+        assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    else:
+        y = hip.gemm_f32(a, b)
+        ref = oracle.gemm(a, b, rows)
+        assert np.linalg.norm(y[rows] - ref) / np.linalg.norm(ref) <= 1e-4
+    assert np.isfinite(y).all()
+
+
+# Large fp16 products whose A rows (odd K, or a base off 4 bytes), B rows
+# (odd N) or both are not 4-byte aligned copy those operands into
+# chunk-padded rows first: A alone, B alone, both through a base offset.
+@pytest.mark.parametrize("mnk_off", [(4096, 8192, 4099, 0), (4096, 8191, 4100, 0),
+                                     (4096, 4096, 4096, 1)])
+def test_gemm_f16_padded_rows(hip, mnk_off):
+    m, n, k, offset = mnk_off
+    a = oracle.to_f16_bits(oracle.uniform(720 + k, (m, k)))
+    b = oracle.to_f16_bits(oracle.uniform(721 + n, (k, n)))
+    rows = tile_row_rows(m, 722)
+    y = hip.gemm_f16(a, b, offset)
+    ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b), rows)
+    assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("mnk", [(300, 301, 999), (1000, 999, 1001), (4096, 4095, 4095),
+                                 (5, 1001, 77)])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_gemm_reads_nothing_past_k_or_the_operands(hip, mnk, dtype):
+    """A and B start NaN-filled allocations, and a few rows of A start with
+    NaN. The copies of a row's last K step run into the next row (and past
+    the end of A and B for the last rows): rows whose own elements are
+    finite must come out finite and equal to the oracle, the NaN rows NaN,
+    and the last elements of A and B (read through a partly out-of-range
+    dword with fp16) must count."""
+    m, n, k = mnk
+    rng = np.random.default_rng(m + 7 * n + k)
+    a = oracle.uniform(710 + m, (m, k))
+    b = oracle.uniform(711 + n, (k, n))
+    a[m - 1, k - 1] = 64.0  # exact in fp16; a lost end element shows at once
+    b[k - 1, n - 1] = -64.0
+    nan_rows = np.unique(rng.integers(1, m, 3)) if m > 2 else np.array([], dtype=np.int64)
+    a[nan_rows, 0] = np.nan
+    if dtype == "f16":
+        a_dev, b_dev = oracle.to_f16_bits(a), oracle.to_f16_bits(b)
+        torch_dtype, fn = torch.float16, hip.lib.operatorlib_gemm_f16
+        a_ref, b_ref = oracle.from_f16_bits(a_dev), oracle.from_f16_bits(b_dev)
+    else:
+        a_dev, b_dev, a_ref, b_ref = a, b, a, b
+        torch_dtype, fn = torch.float32, hip.lib.operatorlib_gemm_f32
+    bufs = []
+    for host in (a_dev, b_dev):
+        buf = torch.full((host.size + 4096,), float("nan"), dtype=torch_dtype, device="cuda")
+        src = torch.from_numpy(host.view(np.float16) if dtype == "f16" else host).reshape(-1)
+        buf[:host.size].copy_(src.to("cuda"))
+        bufs.append(buf)
+    out = empty((m, n))
+    check(fn(ptr(bufs[0]), ptr(bufs[1]), ptr(out), m, n, k, stream_handle()), "gemm")
+    torch.cuda.synchronize()
+    y = out.cpu().numpy().astype(np.float64)
+    finite_rows = np.setdiff1d(np.arange(m), nan_rows)
+    rows = np.unique(np.concatenate([finite_rows[:4], finite_rows[-4:], nan_rows - 1,
+                                     rng.choice(finite_rows, min(24, finite_rows.size),
+                                                replace=False)]))
+    rows = np.setdiff1d(rows, nan_rows)
+    ref = oracle.gemm(np.nan_to_num(a_ref[rows], nan=0.0), b_ref)
+    assert np.isfinite(y[finite_rows]).all()
+    if dtype == "f16":
+        assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    else:
+        assert np.linalg.norm(y[rows] - ref) / np.linalg.norm(ref) <= 1e-4
+    assert np.isnan(y[nan_rows]).all()
 
 
 def test_gemm_pins(hip):

@@ -6,8 +6,8 @@ point's bits; a workspace one byte short must be rejected before anything
 is enqueued (the output keeps its NaN fill). Cases: every launch sequence
 that uses scratch (reduce partials, decode split-K partials on both skinny
 kernels, padded fp16 operands at the 4095^3 BASELINE edge shape, the split
-last round of 256 x 256-tile fp16 and fp32 grids, split fp32 and fp16
-register-staged attention).
+last round of 256 x 256-tile fp16 and fp32 grids, small grids split along
+K, split fp32 and fp16 register-staged attention).
 """
 
 from __future__ import annotations
@@ -64,10 +64,11 @@ def test_reduce_ws_matches_plain(lib, n):
 
 
 # (m, n, k, dtype): narrow decode shapes (split K) on both skinny kernels,
-# padded operands (1000^3, 999 x 1001 x 1003, 4095^3 in both precisions),
-# 272-tile fp16 and fp32 grids whose last round is split, padded operands
-# with a split last round (4097 x 4095 x 4093), small-M grids split along K
-# (64 x 4096 x 4096), shapes that need no scratch.
+# padded fp16 operands (4095^3), unaligned operands read in place (1000^3,
+# 999 x 1001 x 1003, 4095^3 fp32, 500 x 500 x 999), 272-tile fp16 and fp32
+# grids whose last round is split, an unaligned grid with a split last round
+# (4097 x 4095 x 4093), small grids split along K (64 x 4096 x 4096,
+# 1000^3), shapes that need no scratch.
 GEMM_CASES = [(1, 1024, 4096, "f16"), (16, 1024, 4096, "f16"), (1, 1024, 4096, "f32"),
               (16, 1024, 4096, "f32"), (1000, 1000, 1000, "f16"), (4095, 4095, 4095, "f16"),
               (4352, 4096, 512, "f16"), (4352, 4096, 512, "f32"), (1024, 1024, 1024, "f16"),

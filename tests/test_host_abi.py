@@ -213,22 +213,26 @@ def test_gemm_workspace_size(lib):
     assert f32(FAKE, FAKE, 16, 4096, 4096) == 8 * 16 * 4096 * 4  # 64 blocks of 64 x 8
     # 8 column blocks x 64 K splits of 64 rows
     assert f16(FAKE, FAKE, 1, 1024, 4096) == 64 * 1 * 1024 * 4
-    # 4095^3 fp16: A padded to [4095, 4096], B to [4096, 4096]
-    assert f16(FAKE, FAKE, 4095, 4095, 4095) == (4095 * 4096 * 2 + 255) // 256 * 256 + 4096 * 4096 * 2
-    # 4095^3 fp32: A padded to [4095, 4096], B to [4096, 4096]
-    assert f32(FAKE, FAKE, 4095, 4095, 4095) == 4095 * 4096 * 4 + 4096 * 4096 * 4
+    # every other shape reads its operands in place, unaligned ones included,
+    # except large fp16 ones whose rows are not 4-byte aligned: those rows
+    # are copied into chunk-padded rows first (A [M, K'], B [K, N']; with
+    # both copied, K is padded to 64 as well: B [K', N'])
+    assert f16(FAKE, FAKE, 4095, 4095, 4095) == 4095 * 4096 * 2 + 4096 * 4096 * 2
+    assert f16(FAKE, FAKE, 8192, 8192, 8191) == 8192 * 8192 * 2  # A only
+    assert f16(FAKE, FAKE, 4096, 4096, 4095) == 0  # A only, below the one-operand size
+    assert f16(FAKE, FAKE, 4094, 4094, 4094) == 0  # dword-aligned rows
+    assert f32(FAKE, FAKE, 4095, 4095, 4095) == 0
     assert f32(FAKE, FAKE, 4096, 4096, 4096) == 0  # one whole round of 256 tiles
-    # 500 x 500 x 999 fp32: A padded to [500, 1008], B to [1008, 500]
-    assert f32(FAKE, FAKE, 500, 500, 999) == 500 * 1008 * 4 + 1008 * 500 * 4
-    # small fp32 products with short K read the operands in place
+    assert f32(FAKE, FAKE, 500, 500, 999) == 0
+    assert f16(FAKE, FAKE, 333, 777, 999) == 0
     assert f32(FAKE, FAKE, 200, 200, 200) == 0
-    assert f16(NULL, FAKE, 4095, 4095, 4095) == 0  # invalid arguments
+    assert f16(NULL, FAKE, 1, 4096, 4096) == 0  # invalid arguments
 
 
 @pytest.mark.parametrize("bytes_given", [0, 1000])
 def test_gemm_ws_rejects_short_workspace(lib, bytes_given):
     ws = ctypes.c_void_p(0x100000) if bytes_given else NULL
-    assert lib.operatorlib_gemm_f16_ws(FAKE, FAKE, FAKE, 4095, 4095, 4095, ws, bytes_given,
+    assert lib.operatorlib_gemm_f32_ws(FAKE, FAKE, FAKE, 16, 4096, 4096, ws, bytes_given,
                                        NULL) == INVALID
     assert lib.operatorlib_gemm_f16_ws(FAKE, FAKE, FAKE, 1, 1024, 4096, ws, bytes_given,
                                        NULL) == INVALID

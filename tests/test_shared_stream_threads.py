@@ -6,8 +6,8 @@ library together):
   * reduce_sum_f32 over 1,000,003 values (one fp64 partial per workgroup,
     then the combine kernel);
   * gemm_f16 1 x 1024 x 4096 (decode GEMM, split-K partials + split sum);
-  * gemm_f16 1000^3 (K and N not multiples of the fast kernel's steps:
-    zero-padded operand copies, then the product);
+  * gemm_f16 1000^3 (64 tiles of 128 x 128, fewer than the CUs: every
+    tile split along K into partial tiles, then the split sum);
   * attention_f32 B1 H4 S256 D96 (register-staged on a small grid: keys
     split over workgroups, partials, then the combine kernel);
   * gemm_f16 4352 x 4096 x 512 (272 tiles of 256 x 256: the last round's 16
@@ -77,7 +77,7 @@ class Case:
         self.ref = {
             "reduce": oracle.reduce_sum(self.x),
             "skinny": oracle.gemm(f(self.a1), f(self.b1)),
-            "padded": oracle.gemm(f(self.ap), f(self.bp)),
+            "split_k": oracle.gemm(f(self.ap), f(self.bp)),
             "attn": oracle.attention(self.q, self.k, self.v, False),
             "tail": oracle.gemm(f(self.at), f(self.bt), TAIL_ROWS),
         }
@@ -86,7 +86,7 @@ class Case:
         self.out = {
             "reduce": torch.full((rounds,), float("nan"), device="cuda"),
             "skinny": torch.full((rounds, 1, SKINNY_N), float("nan"), device="cuda"),
-            "padded": torch.full((rounds, 1000, 1000), float("nan"), device="cuda"),
+            "split_k": torch.full((rounds, 1000, 1000), float("nan"), device="cuda"),
             "attn": torch.full((rounds, 1, 4, 256, ATTN_D), float("nan"), device="cuda"),
             "tail": torch.full((rounds, TAIL_MK[0], TAIL_N), float("nan"), device="cuda"),
         }
@@ -97,8 +97,8 @@ class Case:
                                              stream), "reduce")
         check(lib.operatorlib_gemm_f16(ptr(d["a1"]), ptr(d["b1"]), ptr(o["skinny"][r]),
                                        1, SKINNY_N, 4096, stream), "gemm_f16 skinny")
-        check(lib.operatorlib_gemm_f16(ptr(d["ap"]), ptr(d["bp"]), ptr(o["padded"][r]),
-                                       1000, 1000, 1000, stream), "gemm_f16 padded")
+        check(lib.operatorlib_gemm_f16(ptr(d["ap"]), ptr(d["bp"]), ptr(o["split_k"][r]),
+                                       1000, 1000, 1000, stream), "gemm_f16 split_k")
         check(lib.operatorlib_attention_f32(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),
                                             ptr(o["attn"][r]), 1, 4, 256, ATTN_D, 0, stream),
               "attention_f32")
@@ -130,8 +130,8 @@ class Case:
                                                 d["x"].numel(), w, nb, stream), "reduce_ws")
         check(lib.operatorlib_gemm_f16_ws(ptr(d["a1"]), ptr(d["b1"]), ptr(o["skinny"][r]),
                                           1, SKINNY_N, 4096, w, nb, stream), "gemm_f16_ws skinny")
-        check(lib.operatorlib_gemm_f16_ws(ptr(d["ap"]), ptr(d["bp"]), ptr(o["padded"][r]),
-                                          1000, 1000, 1000, w, nb, stream), "gemm_f16_ws padded")
+        check(lib.operatorlib_gemm_f16_ws(ptr(d["ap"]), ptr(d["bp"]), ptr(o["split_k"][r]),
+                                          1000, 1000, 1000, w, nb, stream), "gemm_f16_ws split_k")
         check(lib.operatorlib_attention_f32_ws(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),
                                                ptr(o["attn"][r]), 1, 4, 256, ATTN_D, 0, w, nb,
                                                stream), "attention_f32_ws")
@@ -143,14 +143,14 @@ class Case:
         rounds = range(self.out["reduce"].numel()) if rounds is None else rounds
         red = self.out["reduce"].cpu().numpy()
         sk = self.out["skinny"].cpu().numpy().astype(np.float64)
-        pd = self.out["padded"].cpu().numpy().astype(np.float64)
+        pd = self.out["split_k"].cpu().numpy().astype(np.float64)
         at = self.out["attn"].cpu().numpy().astype(np.float64)
         ref = self.ref
         for r in rounds:
             where = f"{label} round {r}"
             assert abs(red[r] - ref["reduce"]) <= 1e-5 * abs(ref["reduce"]), where
             assert np.max(np.abs(sk[r] - ref["skinny"])) <= 2e-3, where
-            assert np.max(np.abs(pd[r] - ref["padded"])) <= 2e-3, where
+            assert np.max(np.abs(pd[r] - ref["split_k"])) <= 2e-3, where
             err = np.abs(at[r] - ref["attn"])
             assert np.all(err <= 1e-4 + 1e-4 * np.abs(ref["attn"])), where
             # deterministic: every round gives the first round's bits

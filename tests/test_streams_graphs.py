@@ -56,7 +56,7 @@ def _all_ops(ops, t):
         ops.softmax(t["sm"].half()),
         ops.rmsnorm(t["rn"].half(), t["w"].half(), 1e-6),
         ops.gemm(t["a"], t["b"]),
-        ops.gemm(t["ah"], t["bh"]),      # zero-padded workspace path
+        ops.gemm(t["ah"], t["bh"]),      # tiles split along K: workspace partials
         ops.gemm(t["a1"], t["b1"]),      # skinny path with K splits
         ops.gemm(t["a16"], t["b1"]),     # matrix-core skinny kernel, vector A
         ops.gemm(t["a1"], t["b1"][:, :1024].contiguous()),   # narrow: more K splits
