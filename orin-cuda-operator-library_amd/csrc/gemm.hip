@@ -1801,12 +1801,16 @@ inline long long round_up(long long x, long long to) { return (x + to - 1) / to 
 // odd N only 968. Dword-aligned: fp16 K = 4094 111, fp32 4095^3 928
 // against 926. Large products therefore first copy such operands into
 // rows padded to a whole number of chunks (about 11.5 us per 4095^2
-// operand): both when both are off (from 10^11 flop, about 3700^3), one
-// alone from 2.75 * 10^11 (about 5200^3). One operand alone is copied with
-// its rows padded to a whole number of chunks (A [M, round_up(K, 8)], B
-// [K, round_up(N, 8)]) and the kernel repairs K's last step itself. Both
-// are also padded along K to a multiple of 64 (A [M, K'], B [K', N'],
-// zeros past K): the kernel then runs its plain schedule.
+// operand). Which ones, measured interleaved (us, median; nothing / A / B
+// / both copied): 4095^3 131.3 / 126.1 / 128.1 / 131.3, 4097 x 4095 x
+// 4093 149.1 / 144.8 / 145.9 / 148.2, 8192 x 8191 x 8191 1104 / 992 /
+// 1044 / 932. So with both off: A alone from 10^11 flop (about 3700^3),
+// both from 4 * 10^11 (about 5800^3); one operand off: that one from
+// 2.75 * 10^11 (about 5200^3). A single copy pads its rows only (A [M,
+// round_up(K, 8)], B [K, round_up(N, 8)]) and the kernel repairs K's last
+// step itself; two copies are also padded along K to a multiple of 64 (A
+// [M, K'], B [K', N'], zeros past K), and the kernel runs its plain
+// schedule.
 struct PadPlan {
   bool pad_a = false, pad_b = false;
   int k = 0;             // the K the kernel runs with
@@ -1826,13 +1830,20 @@ PadPlan pad_plan(const T* a, const T* b, int m, int n, int k) {
     const bool off_a = k % 2 != 0 || !dword(a);
     const bool off_b = n % 2 != 0 || !dword(b);
     const double flops = 2.0 * m * n * static_cast<double>(k);
-    const double from = off_a && off_b ? 1.0e11 : 2.75e11;
-    if ((!off_a && !off_b) || flops < from) return p;
-    const long long kk = off_a && off_b ? round_up(k, 64) : k;  // K the kernel runs with
+    bool pad_a = false, pad_b = false;
+    if (off_a && off_b) {
+      pad_a = flops >= 1.0e11;
+      pad_b = flops >= 4.0e11;
+    } else {
+      pad_a = off_a && flops >= 2.75e11;
+      pad_b = off_b && flops >= 2.75e11;
+    }
+    if (!pad_a && !pad_b) return p;
+    const long long kk = pad_a && pad_b ? round_up(k, 64) : k;  // K the kernel runs with
     const long long kp = round_up(kk, 8), np = round_up(n, 8);
     if (kp > 0x7fffffffLL || np > 0x7fffffffLL) return p;
-    p.pad_a = off_a;
-    p.pad_b = off_b;
+    p.pad_a = pad_a;
+    p.pad_b = pad_b;
     p.k = static_cast<int>(kk);
     if (p.pad_a) {
       p.lda = static_cast<int>(kp);

@@ -710,10 +710,11 @@ def test_gemm_partial_last_step(hip, mnk, dtype):
 
 
 # Large fp16 products whose A rows (odd K, or a base off 4 bytes), B rows
-# (odd N) or both are not 4-byte aligned copy those operands into
-# chunk-padded rows first: A alone, B alone, both through a base offset.
+# (odd N) or both are not 4-byte aligned copy operands into chunk-padded
+# rows first: A alone (odd K), B alone (odd N), A alone with both off at
+# mid size (base offset), both with K padded too (6000 x 6001 x 6003).
 @pytest.mark.parametrize("mnk_off", [(4096, 8192, 4099, 0), (4096, 8191, 4100, 0),
-                                     (4096, 4096, 4096, 1)])
+                                     (4096, 4096, 4096, 1), (6000, 6001, 6003, 0)])
 def test_gemm_f16_padded_rows(hip, mnk_off):
     m, n, k, offset = mnk_off
     a = oracle.to_f16_bits(oracle.uniform(720 + k, (m, k)))

@@ -217,7 +217,8 @@ def test_gemm_workspace_size(lib):
     # except large fp16 ones whose rows are not 4-byte aligned: those rows
     # are copied into chunk-padded rows first (A [M, K'], B [K, N']; with
     # both copied, K is padded to 64 as well: B [K', N'])
-    assert f16(FAKE, FAKE, 4095, 4095, 4095) == 4095 * 4096 * 2 + 4096 * 4096 * 2
+    assert f16(FAKE, FAKE, 4095, 4095, 4095) == 4095 * 4096 * 2  # A only, mid size
+    assert f16(FAKE, FAKE, 8191, 8191, 8191) == 8191 * 8192 * 2 + 8192 * 8192 * 2
     assert f16(FAKE, FAKE, 8192, 8192, 8191) == 8192 * 8192 * 2  # A only
     assert f16(FAKE, FAKE, 4096, 4096, 4095) == 0  # A only, below the one-operand size
     assert f16(FAKE, FAKE, 4094, 4094, 4094) == 0  # dword-aligned rows
