@@ -569,9 +569,6 @@ using SmallTile = Tile<_Float16, 128, 128, 2, 2, 32, 4>;
 using BigTileF32 = Tile<float, 256, 256, 2, 4, 32, 2>;
 using BigTileF32K16 = Tile<float, 256, 256, 2, 4, 16, 4>;
 using SmallTileF32 = Tile<float, 128, 128, 2, 2, 16, 4>;
-// K granularity of every tile configuration of an element type.
-template <typename T>
-constexpr int kBK = sizeof(T) == 2 ? 32 : 16;
 
 template <typename Cfg>
 struct Fragments {
