@@ -207,6 +207,9 @@ TRANSPOSE_SHAPES = [(37, 65), (64, 96), (65, 37), (1, 1), (1, 1000), (1000, 1),
                     (64, 64), (129, 257), (4096, 4096), (4095, 4097),
                     # rows, cols % 4 == 0: the float4 kernel, partial 128-tiles
                     (4, 8), (132, 260), (520, 128), (128, 516), (4, 4096), (1024, 4),
+                    # tile columns past the last whole strip of 16: 22 (a
+                    # partial last tile), 33, 48 (three whole strips)
+                    (384, 2700), (1028, 4100), (260, 6144),
                     # >= 64 tiles of 128x128 at any shape (or offset 1): 16-byte
                     # accesses at 4-byte alignment, element-wise edge float4s;
                     # misaligned input rows (cached loads) ...
