@@ -142,8 +142,8 @@ __device__ __forceinline__ void vec4_tile(const float* __restrict__ input,
   }
 }
 
-// Tile order of transpose_vec4_kernel: strips of kStripTiles tile columns,
-// each walked top to bottom, kStripTiles tiles across per tile row (the
+// Tile order of transpose_vec4_kernel: strips of G = 16 tile columns,
+// each walked top to bottom, G tiles across per tile row (the
 // last strip as wide as the columns left). The ~512 tiles resident at a
 // time (two workgroups per CU) then form a window about as tall as it is
 // wide, so both the input rows read and the output rows written run in
@@ -154,18 +154,20 @@ __device__ __forceinline__ void vec4_tile(const float* __restrict__ input,
 // 262.0 -> 224.0, 16384x4096 103.4 -> 95.4, 2048x16384 54.2 -> 50.9,
 // 1024x8192 15.7 -> 14.5, 8192x4096 45.9 -> 45.4, 4096x4100 27.9 -> 27.1;
 // within 1% either way at 2048^2, 8192x1024, 3000x5000 and 1000^2.
-constexpr int kStripTiles = 16;
-
-template <typename I>
+// transpose_vec4u_kernel takes strips of 8, measured best for it (see
+// there).
+// transpose_window_kernel keeps row-major order (strips of 16 to 48 were
+// 2-7% slower at 4095x4097, 4097x4095 and 8191x8193).
+template <int G, typename I>
 __device__ __forceinline__ void strip_tile(I t, int tiles_x, I tiles_y, int* ty, int* tx) {
-  const int full = tiles_x / kStripTiles * kStripTiles;  // columns in whole strips
+  const int full = tiles_x / G * G;  // columns in whole strips
   const I in_full = static_cast<I>(full) * tiles_y;
   if (t < in_full) {
-    const I per_strip = static_cast<I>(kStripTiles) * tiles_y;
+    const I per_strip = static_cast<I>(G) * tiles_y;
     const I strip = t / per_strip;
     const I r = t - strip * per_strip;
-    *ty = static_cast<int>(r / kStripTiles);
-    *tx = static_cast<int>(strip) * kStripTiles + static_cast<int>(r % kStripTiles);
+    *ty = static_cast<int>(r / G);
+    *tx = static_cast<int>(strip) * G + static_cast<int>(r % G);
   } else {
     const int w = tiles_x - full;
     const I r = t - in_full;
@@ -182,9 +184,9 @@ __global__ __launch_bounds__(kThreads) void transpose_vec4_kernel(
   for (long long t = blockIdx.x; t < tiles; t += gridDim.x) {
     int ty, tx;  // 32-bit division whenever the tile count allows
     if (tiles <= 0x7fffffffLL)
-      strip_tile<int>(static_cast<int>(t), tiles_x, static_cast<int>(tiles_y), &ty, &tx);
+      strip_tile<16, int>(static_cast<int>(t), tiles_x, static_cast<int>(tiles_y), &ty, &tx);
     else
-      strip_tile<long long>(t, tiles_x, tiles_y, &ty, &tx);
+      strip_tile<16, long long>(t, tiles_x, tiles_y, &ty, &tx);
     const int row0 = ty * kVecTile;
     const int col0 = tx * kVecTile;
     if (row0 + kVecTile <= rows && col0 + kVecTile <= cols)
@@ -279,9 +281,17 @@ __global__ __launch_bounds__(kThreads) void transpose_vec4u_kernel(
     const float* __restrict__ input, float* __restrict__ output, int rows,
     int cols, int tiles_x, long long tiles) {
   __shared__ float tile[kVecTile * kVecPitch];
+  const long long tiles_y = tiles / tiles_x;
   for (long long t = blockIdx.x; t < tiles; t += gridDim.x) {
-    const int ty = static_cast<int>(t / tiles_x);
-    const int tx = static_cast<int>(t % tiles_x);
+    // strips of 8 tile columns (strip_tile); measured on MI355X (us,
+    // row-major -> strips of 8; 12, 16 and 24 were no better overall):
+    // 4096x4095 28.0 -> 26.4, 4096x4097 27.2 -> 26.1, 8192x8191 105.3 ->
+    // 94.2, 2048x6001 20.6 -> 20.5
+    int ty, tx;
+    if (tiles <= 0x7fffffffLL)
+      strip_tile<8, int>(static_cast<int>(t), tiles_x, static_cast<int>(tiles_y), &ty, &tx);
+    else
+      strip_tile<8, long long>(t, tiles_x, tiles_y, &ty, &tx);
     const int row0 = ty * kVecTile;
     const int col0 = tx * kVecTile;
     if (row0 + kVecTile <= rows && col0 + kVecTile <= cols)
