@@ -576,7 +576,7 @@ struct Fragments {
   typename Cfg::Frag b[Cfg::kFN];
 };
 
-template <typename Cfg, bool kTail = false, bool kEdge = false>
+template <typename Cfg, bool kTail = false, bool kEdge = false, bool kStreamC = false>
 __global__ __launch_bounds__(Cfg::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
                      const typename Cfg::Type* __restrict__ B,
@@ -872,6 +872,66 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
     asm volatile("s_barrier" ::: "memory");
   };
 
+  // A tail part writes its whole tile, row-major, to its partial slot;
+  // sum_tail_kernel adds the parts in split order.
+  float* const out = split >= 0
+      ? tail.partial + static_cast<std::size_t>(split * tail.tiles + tail_index) * kBM * kBN
+      : C + static_cast<std::size_t>(m0) * N + n0;
+  const int ldo = split >= 0 ? kBN : N;
+  // (a part's rows past M are never summed, so they are not written)
+  const int row_end = min(kBM, M - m0);
+  const int col_end = split >= 0 ? kBN : N - n0;
+  const bool full = row_end >= kBM && col_end >= kBN;
+  // Whole fp16 256 x 256 tiles of the two-stage configuration leave through
+  // LDS: each wavefront writes 32 rows of its 128 x 64 sub-tile at a time
+  // into its own 8.5 KiB block (68-float rows: the accumulator layout's
+  // four row groups of a write land on different banks, and rows stay
+  // 16-byte aligned), then reads them back row-major and stores 16 bytes
+  // per lane, four 256-byte row segments per instruction: 32 store
+  // instructions per lane instead of 128 single-float ones, each writing
+  // whole cache lines (which the non-temporal stores need). Measured on
+  // MI355X (us, per-float -> staged, cached stores): 4096^3 106.8 -> 104.0,
+  // 8192^3 866 -> 852, 8192^2 x 2048 241 -> 227, 8192^2 x 4096 424 -> 406,
+  // 16384^2 x 4096 1906 -> 1811. (fp32 keeps the per-float stores: with
+  // the staged ones its main loop compiled slower, 4096^3 923 -> 1242.)
+  constexpr bool kStagedOut = kSize == 2 && Cfg::kStages == 2 && kBM == 256 && kBN == 256 &&
+                              kFM == 8 && kFN == 4;
+  constexpr int kOutPitch = 68;                       // floats per staged row
+  constexpr int kOutBlock = 32 * kOutPitch * 4;       // bytes per wavefront
+  static_assert(!kStagedOut || 4 * kOutBlock <= Cfg::kStage, "four blocks per stage array");
+  const bool staged = kStagedOut && full && ldo % 4 == 0 &&
+                      (reinterpret_cast<std::uintptr_t>(out) & 15) == 0;
+  auto store_staged = [&](unsigned char* lo, unsigned char* hi) {
+    // every wave's last reads and copies are done before any block is written
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("s_barrier" ::: "memory");
+    OPL_LDS float* const blk =
+        (OPL_LDS float*)((wave < 4 ? lo : hi) + (wave % 4) * kOutBlock);
+    float* const wout = out + static_cast<std::size_t>(wm * (kBM / kWM)) * ldo + wn * (kBN / kWN);
+#pragma unroll
+    for (int q = 0; q < kFM / 2; ++q) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int tj = 0; tj < kFN; ++tj)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            blk[(16 * t + 4 * group + e) * kOutPitch + 16 * tj + gl] = acc[2 * q + t][tj][e];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = 4 * i + lane / 16;
+        const int c4 = lane % 16;
+        const floatx4 v = *(const OPL_LDS floatx4*)(blk + row * kOutPitch + 4 * c4);
+        floatx4* const p =
+            reinterpret_cast<floatx4*>(wout + static_cast<std::size_t>(32 * q + row) * ldo + 4 * c4);
+        if constexpr (kStreamC)
+          __builtin_nontemporal_store(v, p);
+        else
+          *p = v;
+      }
+    }
+  };
+
   Fragments<Cfg> f0, f1;
   if constexpr (Cfg::kStages == 2) {
     __shared__ __attribute__((aligned(1024))) unsigned char stage0[Cfg::kStage];
@@ -920,6 +980,12 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
       tile(stage1, stage0, step + 1);
     }
     if (step < steps) tile(stage0, stage1, step);
+    if constexpr (kStagedOut) {
+      if (staged) {
+        store_staged(stage0, stage1);
+        return;
+      }
+    }
   } else {
     __shared__ __attribute__((aligned(1024))) unsigned char stage0[Cfg::kStage];
     __shared__ __attribute__((aligned(1024))) unsigned char stage1[Cfg::kStage];
@@ -966,16 +1032,6 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
   }
   __builtin_amdgcn_s_waitcnt(0);  // the last (empty) copies
 
-  // A tail part writes its whole tile, row-major, to its partial slot;
-  // sum_tail_kernel adds the parts in split order.
-  float* const out = split >= 0
-      ? tail.partial + static_cast<std::size_t>(split * tail.tiles + tail_index) * kBM * kBN
-      : C + static_cast<std::size_t>(m0) * N + n0;
-  const int ldo = split >= 0 ? kBN : N;
-  // (a part's rows past M are never summed, so they are not written)
-  const int row_end = min(kBM, M - m0);
-  const int col_end = split >= 0 ? kBN : N - n0;
-  const bool full = row_end >= kBM && col_end >= kBN;
 #pragma unroll
   for (int ti = 0; ti < kFM; ++ti) {
 #pragma unroll
@@ -984,8 +1040,15 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = wm * (kBM / kWM) + 16 * ti + 4 * group + e;
-        if (full || (row < row_end && col < col_end))
-          out[static_cast<std::size_t>(row) * ldo + col] = acc[ti][tj][e];
+        if (full || (row < row_end && col < col_end)) {
+          float* const p = out + static_cast<std::size_t>(row) * ldo + col;
+          // (a compile-time choice: under a run-time branch the compiler
+          // merges the two stores and drops the non-temporal hint)
+          if constexpr (kStreamC)
+            __builtin_nontemporal_store(acc[ti][tj][e], p);
+          else
+            *p = acc[ti][tj][e];
+        }
       }
     }
   }
@@ -1903,6 +1966,8 @@ int staging_for(const T* a, const T* b, int n, int k) {
   return dword_rows ? kDword : kElementwise;
 }
 
+int device_cus();
+
 template <typename Cfg>
 hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Type* b, float* c,
                             int m, int n, int k, int lda, int ldb, hipStream_t stream,
@@ -1916,6 +1981,25 @@ hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Typ
   // run the instance that repairs that step (the others keep the plain
   // schedule: the repair's code cost the aligned 4096^3 product 2%).
   const bool edge = k % Cfg::kBK != 0 || (sizeof(typename Cfg::Type) == 2 && (lda % 2 != 0 || ldb % 2 != 0));
+  // C is stored non-temporally when later rounds re-read operand panels
+  // that cached C lines would evict: fp16 256 x 256 grids (whose whole
+  // tiles leave through LDS as full cache lines) of two or more rounds,
+  // with A and B together past three quarters of the 256 MiB Infinity
+  // Cache. Measured on MI355X (us, cached -> non-temporal, both with the
+  // staged epilogue): 8192^3 (A + B 256 MiB) 852 -> 770; 16384^2 x 4096
+  // (256 MiB) 1811 -> 1604; 12288^2 x 8192 (384 MiB) 1945 -> 1741;
+  // 8192^2 x 4096 (128 MiB) 405.5 -> 404.9; 8192^2 x 2048 (64 MiB) 226.6
+  // -> 230.2; 4096 x 8192 x 4096 (96 MiB) 202.4 -> 207.0; single rounds
+  // (4096^3 104.0 -> 108.2, 4095^3 128 -> 166) and C rows off 16-byte
+  // alignment (8191^3, per-float stores: 948 -> 1063) lose.
+  const long long operand_bytes =
+      (static_cast<long long>(m) * lda + static_cast<long long>(k) * ldb) *
+      static_cast<long long>(sizeof(typename Cfg::Type));
+  const bool stream_c = sizeof(typename Cfg::Type) == 2 && Cfg::kBM == 256 &&
+                        Cfg::kStages == 2 && tail.splits == 0 && n % 4 == 0 &&
+                        (reinterpret_cast<std::uintptr_t>(c) & 15) == 0 &&
+                        operand_bytes >= (192LL << 20) && device_cus() > 0 &&
+                        tiles >= 2LL * device_cus();
   const dim3 grid(static_cast<unsigned>(blocks)), block(Cfg::kThreads);
   if (tail.splits > 0) {
     if (edge)
@@ -1926,6 +2010,13 @@ hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Typ
                                                                   tail);
     dma::sum_tail_kernel<Cfg><<<dim3(Cfg::kBM * Cfg::kBN / 4 / 256, tail.tiles), dim3(256), 0,
                                 stream>>>(c, m, n, tail);
+  } else if (stream_c) {
+    if (edge)
+      dma::gemm_dma_kernel<Cfg, false, true, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k,
+                                                                             lda, ldb, tail);
+    else
+      dma::gemm_dma_kernel<Cfg, false, false, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k,
+                                                                              lda, ldb, tail);
   } else if (edge) {
     dma::gemm_dma_kernel<Cfg, false, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k, lda,
                                                                        ldb, tail);
