@@ -882,9 +882,9 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
   const int row_end = min(kBM, M - m0);
   const int col_end = split >= 0 ? kBN : N - n0;
   const bool full = row_end >= kBM && col_end >= kBN;
-  // Whole fp16 256 x 256 tiles of the two-stage configuration leave through
-  // LDS: each wavefront writes 32 rows of its 128 x 64 sub-tile at a time
-  // into its own 8.5 KiB block (68-float rows: the accumulator layout's
+  // Whole fp16 tiles leave through LDS: each wavefront writes 32 rows of
+  // its 128 x 64 (or 64 x 64) sub-tile at a time into its own 8.5 KiB
+  // block (68-float rows: the accumulator layout's
   // four row groups of a write land on different banks, and rows stay
   // 16-byte aligned), then reads them back row-major and stores 16 bytes
   // per lane, four 256-byte row segments per instruction: 32 store
@@ -894,19 +894,28 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
   // 8192^3 866 -> 852, 8192^2 x 2048 241 -> 227, 8192^2 x 4096 424 -> 406,
   // 16384^2 x 4096 1906 -> 1811. (fp32 keeps the per-float stores: with
   // the staged ones its main loop compiled slower, 4096^3 923 -> 1242.)
-  constexpr bool kStagedOut = kSize == 2 && Cfg::kStages == 2 && kBM == 256 && kBN == 256 &&
-                              kFM == 8 && kFN == 4;
+  constexpr int kWaves = kWM * kWN;
   constexpr int kOutPitch = 68;                       // floats per staged row
   constexpr int kOutBlock = 32 * kOutPitch * 4;       // bytes per wavefront
-  static_assert(!kStagedOut || 4 * kOutBlock <= Cfg::kStage, "four blocks per stage array");
+  constexpr int kBlocksPerStage = kWaves / Cfg::kStages;  // wavefront blocks per stage array
+  // (not the four-stage 256 x 256 instance, K % 64 == 32, which already
+  // runs at the 256-VGPR limit)
+  constexpr bool kStagedOut = kSize == 2 && kFN == 4 && kFM % 2 == 0 &&
+                              (Cfg::kStages == 2 || kWaves == 4) &&
+                              kWaves % Cfg::kStages == 0 &&
+                              kBlocksPerStage * kOutBlock <= Cfg::kStage;
   const bool staged = kStagedOut && full && ldo % 4 == 0 &&
                       (reinterpret_cast<std::uintptr_t>(out) & 15) == 0;
-  auto store_staged = [&](unsigned char* lo, unsigned char* hi) {
+  // st: the stage arrays in order (the last two unused with two stages).
+  auto store_staged = [&](unsigned char* s0, unsigned char* s1, unsigned char* s2,
+                          unsigned char* s3) {
     // every wave's last reads and copies are done before any block is written
     __builtin_amdgcn_s_waitcnt(0);
     asm volatile("s_barrier" ::: "memory");
+    const int array = wave / kBlocksPerStage;
+    unsigned char* const base = array == 0 ? s0 : array == 1 ? s1 : array == 2 ? s2 : s3;
     OPL_LDS float* const blk =
-        (OPL_LDS float*)((wave < 4 ? lo : hi) + (wave % 4) * kOutBlock);
+        (OPL_LDS float*)(base + (wave % kBlocksPerStage) * kOutBlock);
     float* const wout = out + static_cast<std::size_t>(wm * (kBM / kWM)) * ldo + wn * (kBN / kWN);
 #pragma unroll
     for (int q = 0; q < kFM / 2; ++q) {
@@ -982,7 +991,7 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
     if (step < steps) tile(stage0, stage1, step);
     if constexpr (kStagedOut) {
       if (staged) {
-        store_staged(stage0, stage1);
+        store_staged(stage0, stage1, stage0, stage1);
         return;
       }
     }
@@ -1029,6 +1038,12 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
     if (step < steps) tile(stage0, stage1, step, f0, f1);
     if (step + 1 < steps) tile(stage1, stage2, step + 1, f1, f0);
     if (step + 2 < steps) tile(stage2, stage3, step + 2, f0, f1);
+    if constexpr (kStagedOut) {
+      if (staged) {
+        store_staged(stage0, stage1, stage2, stage3);
+        return;
+      }
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);  // the last (empty) copies
 
