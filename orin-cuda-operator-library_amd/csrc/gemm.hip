@@ -904,8 +904,9 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
                               (Cfg::kStages == 2 || kWaves == 4) &&
                               kWaves % Cfg::kStages == 0 &&
                               kBlocksPerStage * kOutBlock <= Cfg::kStage;
-  const bool staged = kStagedOut && full && ldo % 4 == 0 &&
-                      (reinterpret_cast<std::uintptr_t>(out) & 15) == 0;
+  // (any row length: the 16-byte stores need only 4-byte alignment under
+  // the target's unaligned access mode)
+  const bool staged = kStagedOut && full;
   // st: the stage arrays in order (the last two unused with two stages).
   auto store_staged = [&](unsigned char* s0, unsigned char* s1, unsigned char* s2,
                           unsigned char* s3) {
@@ -931,8 +932,9 @@ void gemm_dma_kernel(const typename Cfg::Type* __restrict__ A,
         const int row = 4 * i + lane / 16;
         const int c4 = lane % 16;
         const floatx4 v = *(const OPL_LDS floatx4*)(blk + row * kOutPitch + 4 * c4);
-        floatx4* const p =
-            reinterpret_cast<floatx4*>(wout + static_cast<std::size_t>(32 * q + row) * ldo + 4 * c4);
+        typedef float floatx4u __attribute__((ext_vector_type(4), aligned(4)));
+        floatx4u* const p = reinterpret_cast<floatx4u*>(
+            wout + static_cast<std::size_t>(32 * q + row) * ldo + 4 * c4);
         if constexpr (kStreamC)
           __builtin_nontemporal_store(v, p);
         else
@@ -2011,8 +2013,7 @@ hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Typ
       (static_cast<long long>(m) * lda + static_cast<long long>(k) * ldb) *
       static_cast<long long>(sizeof(typename Cfg::Type));
   const bool stream_c = sizeof(typename Cfg::Type) == 2 && Cfg::kBM == 256 &&
-                        Cfg::kStages == 2 && tail.splits == 0 && n % 4 == 0 &&
-                        (reinterpret_cast<std::uintptr_t>(c) & 15) == 0 &&
+                        Cfg::kStages == 2 && tail.splits == 0 &&
                         operand_bytes >= (192LL << 20) && device_cus() > 0 &&
                         tiles >= 2LL * device_cus();
   const dim3 grid(static_cast<unsigned>(blocks)), block(Cfg::kThreads);
