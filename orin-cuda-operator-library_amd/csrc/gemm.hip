@@ -445,10 +445,14 @@ void gemm_mfma_kernel(const T* __restrict__ A, const T* __restrict__ B,
 //     MI355X: fp32 4095^3 925 against 979 on padded copies; fp16 4096 x
 //     4096 x 4095 114 against 128; 1000^3 19 against 32; 100^3 6 against
 //     15).
-// Measured on MI355X (median of 8-launch groups): 4096^3 104-109 us, 8192^3
-// 852-871 us (1.26-1.29 PFLOP/s); hipBLASLt with the same fp32 C: 112-116
-// and 827-859 us. With v_mfma_f32_32x32x16_f16 the same schedule ran
-// 111-119 / 890-910 us, bit-identical output.
+//   * C leaves through LDS as full-line 16-byte stores, non-temporal on
+//     grids of two or more rounds with large operands (store_staged and
+//     the launcher's stream_c rule).
+// Measured on MI355X (median of 8-launch groups): 4096^3 100-105 us, 8192^3
+// 740-780 us (1.41-1.49 PFLOP/s); hipBLASLt with the same fp32 C: 114 and
+// 853-856 us. Before the staged epilogue: 104-109 / 852-871 us. With
+// v_mfma_f32_32x32x16_f16 the same schedule ran 111-119 / 890-910 us,
+// bit-identical output.
 //
 // fp32: the same tiles, stages and schedule with the same A row bytes per
 // step (32 or 16 elements), on v_mfma_f32_16x16x4_f32. A fragments are the
