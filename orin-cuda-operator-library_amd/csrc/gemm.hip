@@ -1737,7 +1737,11 @@ __global__ __launch_bounds__(kThreads) void narrow_kernel(const T* __restrict__ 
       const int cc = in ? c : 0;
 #pragma unroll
       for (int r = 0; r < kRows; ++r)
-        a[u][r] = *reinterpret_cast<const Vec*>(arow[r] + static_cast<std::size_t>(cc) * E);
+        // A is streamed once: non-temporal loads (MI355X, us, cached ->
+        // non-temporal: fp16 4096 x 1 x 4096 8.62 -> 8.19, 4096 x 16 x 4096
+        // 22.88 -> 22.49; fp32 4096 x 1 x 4096 17.23 -> 16.93)
+        a[u][r] = __builtin_nontemporal_load(
+            reinterpret_cast<const Vec*>(arow[r] + static_cast<std::size_t>(cc) * E));
       const T* bblk = B + static_cast<std::size_t>(cc) * E * N;
 #pragma unroll
       for (int j = 0; j < N; ++j) b[u][j] = *reinterpret_cast<const Vec*>(bblk + E * j);
