@@ -2028,15 +2028,16 @@ hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Typ
   // (256 MiB) 1811 -> 1604; 12288^2 x 8192 (384 MiB) 1945 -> 1741;
   // 8192^2 x 4096 (128 MiB) 405.5 -> 404.9; 8192^2 x 2048 (64 MiB) 226.6
   // -> 230.2; 4096 x 8192 x 4096 (96 MiB) 202.4 -> 207.0; single rounds
-  // (4096^3 104.0 -> 108.2, 4095^3 128 -> 166) and C rows off 16-byte
-  // alignment (8191^3, per-float stores: 948 -> 1063) lose.
+  // lose (4096^3 104.0 -> 108.2, 4095^3 128 -> 166). Rows at any 4-byte
+  // phase stream too: 8191^3 948 -> 920 with the staged stores (the
+  // per-float stores had lost there, 948 -> 1063).
+  constexpr bool kCanStream =
+      sizeof(typename Cfg::Type) == 2 && Cfg::kBM == 256 && Cfg::kStages == 2;
   const long long operand_bytes =
       (static_cast<long long>(m) * lda + static_cast<long long>(k) * ldb) *
       static_cast<long long>(sizeof(typename Cfg::Type));
-  const bool stream_c = sizeof(typename Cfg::Type) == 2 && Cfg::kBM == 256 &&
-                        Cfg::kStages == 2 && tail.splits == 0 &&
-                        operand_bytes >= (192LL << 20) && device_cus() > 0 &&
-                        tiles >= 2LL * device_cus();
+  const bool stream_c = kCanStream && tail.splits == 0 && operand_bytes >= (192LL << 20) &&
+                        device_cus() > 0 && tiles >= 2LL * device_cus();
   const dim3 grid(static_cast<unsigned>(blocks)), block(Cfg::kThreads);
   if (tail.splits > 0) {
     if (edge)
@@ -2048,12 +2049,14 @@ hipError_t launch_dma_tiles(const typename Cfg::Type* a, const typename Cfg::Typ
     dma::sum_tail_kernel<Cfg><<<dim3(Cfg::kBM * Cfg::kBN / 4 / 256, tail.tiles), dim3(256), 0,
                                 stream>>>(c, m, n, tail);
   } else if (stream_c) {
-    if (edge)
-      dma::gemm_dma_kernel<Cfg, false, true, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k,
-                                                                             lda, ldb, tail);
-    else
-      dma::gemm_dma_kernel<Cfg, false, false, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k,
-                                                                              lda, ldb, tail);
+    if constexpr (kCanStream) {
+      if (edge)
+        dma::gemm_dma_kernel<Cfg, false, true, true><<<grid, block, 0, stream>>>(
+            a, b, c, m, n, k, lda, ldb, tail);
+      else
+        dma::gemm_dma_kernel<Cfg, false, false, true><<<grid, block, 0, stream>>>(
+            a, b, c, m, n, k, lda, ldb, tail);
+    }
   } else if (edge) {
     dma::gemm_dma_kernel<Cfg, false, true><<<grid, block, 0, stream>>>(a, b, c, m, n, k, lda,
                                                                        ldb, tail);
