@@ -815,6 +815,24 @@ def test_gemm_baseline_sizes(hip, dtype, size):
     assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize("m,n,k", [(8191, 8191, 8191), (8192, 8190, 8192)])
+def test_gemm_f16_streaming_c_odd_rows(hip, m, n, k):
+    # Four rounds of 256 x 256 tiles with A + B past 192 MiB: C is stored
+    # non-temporally through the LDS-staged epilogue, here with C rows off
+    # 16-byte alignment (N = 8191, 8190), A / B rows at a 2-byte phase
+    # (8191: the edge instance) and partial edge tiles on the per-float path.
+    rng = np.random.default_rng(811)
+    a = oracle.to_f16_bits(oracle.uniform(812, (m, k)))
+    b = oracle.to_f16_bits(oracle.uniform(813, (k, n)))
+    bands = np.arange(0, m, 256)
+    picks = np.minimum(bands + rng.integers(0, 256, bands.size), m - 1)
+    rows = np.unique(np.concatenate([[0, 1, m - 2, m - 1], picks])).astype(np.int32)
+    y = hip.gemm_f16(a, b)
+    ref = oracle.gemm(oracle.from_f16_bits(a), oracle.from_f16_bits(b), rows)
+    assert np.max(np.abs(y[rows] - ref)) <= 2e-3
+    assert np.isfinite(y).all()
+
+
 # --------------------------------------------------------------------- attention
 
 # (S, D, causal, extreme): tests/attention_smoke.cu:168-173, edge shapes, and
