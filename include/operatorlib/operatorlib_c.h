@@ -14,9 +14,10 @@
  * synchronization, as with any asynchronous HIP work.
  *
  * Device memory: the library never allocates. Launch sequences that need
- * scratch beyond the caller's buffers (reduce partials, split-K partial
- * sums, padded GEMM operands, split attention partials) take it from one
- * of two places:
+ * scratch beyond the caller's buffers (reduce partials, per-segment
+ * partials of softmax and RMSNorm rows split over workgroups, split-K
+ * partial sums, padded GEMM operands, split attention partials) take it
+ * from one of two places:
  *   - the plain entry points: a static array of 256 MiB per GPU (the
  *     "arena"), held from the library's load to process exit. Calls that
  *     use it on different streams are ordered on the device by an event
@@ -152,6 +153,41 @@ int operatorlib_rmsnorm_f16(const operatorlib_half_t* input,
                             const operatorlib_half_t* weight,
                             operatorlib_half_t* output, int tokens,
                             int hidden, float epsilon, void* stream);
+
+/*
+ * Workspace forms of the softmax and RMSNorm entry points (see the top of
+ * this file). Rows longer than 32768 columns, and fewer than 64 rows longer
+ * than 4096, are cut into segments over workgroups whose partials (8 bytes
+ * per row and segment for softmax, 4 for RMSNorm) go to scratch; every
+ * other shape needs none (the queries return 0). The result bits are those
+ * of the plain forms.
+ * Errors: as the plain forms; a workspace smaller than the query's answer,
+ * or NULL or not 256-byte aligned when that is non-zero. The queries
+ * return 0 for invalid sizes.
+ * No counterpart in the reference (src/softmax.cu:182-202 and
+ * src/rmsnorm.cu:77-95 need no scratch): for callers that own all device
+ * memory.
+ */
+size_t operatorlib_softmax_f32_workspace_size(int rows, int cols);
+int operatorlib_softmax_f32_ws(const float* input, float* output, int rows,
+                               int cols, void* workspace,
+                               size_t workspace_bytes, void* stream);
+size_t operatorlib_softmax_f16_workspace_size(int rows, int cols);
+int operatorlib_softmax_f16_ws(const operatorlib_half_t* input,
+                               operatorlib_half_t* output, int rows, int cols,
+                               void* workspace, size_t workspace_bytes,
+                               void* stream);
+size_t operatorlib_rmsnorm_f32_workspace_size(int tokens, int hidden);
+int operatorlib_rmsnorm_f32_ws(const float* input, const float* weight,
+                               float* output, int tokens, int hidden,
+                               float epsilon, void* workspace,
+                               size_t workspace_bytes, void* stream);
+size_t operatorlib_rmsnorm_f16_workspace_size(int tokens, int hidden);
+int operatorlib_rmsnorm_f16_ws(const operatorlib_half_t* input,
+                               const operatorlib_half_t* weight,
+                               operatorlib_half_t* output, int tokens,
+                               int hidden, float epsilon, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /*
  * Row-major C[m, n] = A[m, k] * B[k, n], fp32 in / fp32 out.

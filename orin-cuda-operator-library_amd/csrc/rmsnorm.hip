@@ -13,7 +13,8 @@
 // to 32768), so x is read from HBM once and y written once; w (one row of
 // bytes) is shared by all rows and served from L2/MALL after first touch.
 // Algorithmic traffic: (2 * tokens * hidden + hidden) * sizeof(element).
-// Only rows longer than 32768 columns re-read x (two passes).
+// Rows longer than 32768 columns, and a few long rows that would leave CUs
+// idle, are cut into segments over workgroups and re-read x once.
 
 #include <hip/hip_runtime.h>
 
@@ -22,6 +23,7 @@
 #include "common.hpp"
 #include "operatorlib/operatorlib_c.h"
 #include "rowwise.hpp"
+#include "scratch.hpp"
 #include "validate.hpp"
 
 namespace {
@@ -181,24 +183,200 @@ __global__ __launch_bounds__(opl::kRowBlockThreads) void rmsnorm_ragged_block_ke
       output + offset, cols, threadIdx.x, inv);
 }
 
-template <typename T>
-__global__ __launch_bounds__(opl::kRowBlockThreads) void rmsnorm_two_pass_kernel(
+// Short rows: a group of G lanes per row, 64 / G rows per wavefront, one
+// access per lane (W = E: chunk t of aligned rows; W = 1: element t). A
+// lane's weights are the same for every row it visits, so they are loaded
+// once. A wavefront per row left most lanes idle here (1048576 x 16: 151 us
+// against a 19.5 us copy of the same bytes).
+template <typename T, int G, int W, int U>
+__global__ __launch_bounds__(opl::kGroupThreads) void rmsnorm_group_kernel(
     const T* __restrict__ input, const T* __restrict__ weight,
-    T* __restrict__ output, int cols, float epsilon) {
-  __shared__ float slots[opl::kRowBlockWaves];
-  const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
-  const T* row = input + offset;
-  T* out = output + offset;
+    T* __restrict__ output, int rows, int cols, float epsilon) {
+  using A = typename opl::Access<T, W>::type;
+  constexpr int kRowsPerWave = opl::kWaveSize / G;
+  constexpr int kWaves = opl::kGroupThreads / opl::kWaveSize;
+  const int lane = threadIdx.x % opl::kWaveSize;
+  const int t = lane % G;
+  const int r_lane = lane / G;
+  const bool lane_in = t * W < cols;
+  const A wq = *reinterpret_cast<const A*>(weight + (lane_in ? t * W : 0));
+  const long long stride = static_cast<long long>(gridDim.x) * kWaves * kRowsPerWave * U;
+  for (long long r0 = (static_cast<long long>(blockIdx.x) * kWaves + threadIdx.x / opl::kWaveSize) *
+                      kRowsPerWave * U;
+       r0 < rows; r0 += stride) {
+    A q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long row = r0 + u * kRowsPerWave + r_lane;
+      const bool in = lane_in && row < rows;
+      q[u] = __builtin_nontemporal_load(
+          reinterpret_cast<const A*>(input + (in ? row * cols + t * W : 0)));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long row = r0 + u * kRowsPerWave + r_lane;
+      const bool in = lane_in && row < rows;
+      float x[W];
+#pragma unroll
+      for (int e = 0; e < W; ++e) x[e] = in ? static_cast<float>(q[u][e]) : 0.0f;
+      const float ss = opl::group_reduce<opl::SumOp, G>(sum_squares(x));
+      const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
+      if (in) {
+        A y;
+#pragma unroll
+        for (int e = 0; e < W; ++e) y[e] = static_cast<T>((x[e] * inv) * static_cast<float>(wq[e]));
+        __builtin_nontemporal_store(y, reinterpret_cast<A*>(output + row * cols + t * W));
+      }
+    }
+  }
+}
+
+template <typename T, int W, int U, int G = 1>
+void launch_group(int g, const T* in, const T* w, T* out, int rows, int cols, float eps,
+                  hipStream_t stream) {
+  if constexpr (G < 32) {
+    if (g > G) return launch_group<T, W, U, 2 * G>(g, in, w, out, rows, cols, eps, stream);
+  }
+  constexpr int kRowsPerBlock = opl::kGroupThreads / G * U;
+  const long long blocks = (static_cast<long long>(rows) + kRowsPerBlock - 1) / kRowsPerBlock;
+  rmsnorm_group_kernel<T, G, W, U>
+      <<<dim3(static_cast<unsigned>(blocks < opl::kGroupMaxBlocks ? blocks : opl::kGroupMaxBlocks)),
+         dim3(opl::kGroupThreads), 0, stream>>>(in, w, out, rows, cols, eps);
+}
+
+// Rows over several workgroups (opl::split_plan: rows too long for
+// registers, and few long rows; one workgroup per row took 1076 us for 4 x
+// 2^20 and 42 us for 64 x 65536). Pass 1 writes every segment's sum of
+// squares to scratch; pass 2 sums the row's partials in segment order
+// (every wavefront of the row computes the same bits), re-reads its
+// segment and writes (x * inv) * w.
+using opl::kSplitThreads;
+using opl::kSplitUnroll;
+using opl::kSplitWaves;
+
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void rmsnorm_split_stats_kernel(
+    const T* __restrict__ input, float* __restrict__ partials, int cols, int seg_len) {
+  using Chunk = typename opl::RowElem<T>::Chunk;
+  constexpr int E = opl::RowElem<T>::kPerChunk;
+  __shared__ float slots[kSplitWaves];
+  const int c0 = blockIdx.x * seg_len;
+  const int n = min(cols - c0, seg_len);
+  const T* p = input + static_cast<std::size_t>(blockIdx.y) * cols + c0;
+  const opl::Segment<T> sg(p, n);
+  const Chunk* body = reinterpret_cast<const Chunk*>(p + sg.head);
+  const int t = threadIdx.x;
   float ss = 0.0f;
-  for (int c = threadIdx.x; c < cols; c += opl::kRowBlockThreads) {
-    const float x = static_cast<float>(row[c]);
+  for (int i0 = t; i0 < sg.body; i0 += kSplitThreads * kSplitUnroll) {
+    Chunk q[kSplitUnroll];
+#pragma unroll
+    for (int u = 0; u < kSplitUnroll; ++u) {
+      const int i = i0 + u * kSplitThreads;
+      q[u] = body[i < sg.body ? i : i0];  // cached: pass 2 reads it again
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitUnroll; ++u) {
+      if (i0 + u * kSplitThreads < sg.body) {
+        float x[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = static_cast<float>(q[u][e]);
+        ss += sum_squares(x);
+      }
+    }
+  }
+  const int xc = sg.extra(t);
+  if (xc >= 0) {
+    const float x = static_cast<float>(p[xc]);
     ss += x * x;
   }
-  ss = opl::block_reduce<opl::SumOp, opl::kRowBlockWaves>(ss, slots);
-  const float inv = rsqrtf(ss / static_cast<float>(cols) + epsilon);
-  for (int c = threadIdx.x; c < cols; c += opl::kRowBlockThreads)
-    out[c] = static_cast<T>((static_cast<float>(row[c]) * inv) *
-                            static_cast<float>(weight[c]));
+  ss = opl::block_reduce<opl::SumOp, kSplitWaves>(ss, slots);
+  if (t == 0) partials[static_cast<std::size_t>(blockIdx.y) * gridDim.x + blockIdx.x] = ss;
+}
+
+// kChunks: input and output rows share their 16-byte phase (16-byte
+// accesses on both sides; the weights as chunks too where their phase is
+// the row's, else element by element from the caches); otherwise element
+// accesses.
+template <typename T, bool kChunks>
+__global__ __launch_bounds__(kSplitThreads) void rmsnorm_split_apply_kernel(
+    const T* __restrict__ input, const T* __restrict__ weight, T* __restrict__ output,
+    const float* __restrict__ partials, int cols, int seg_len, float epsilon) {
+  using Chunk = typename opl::RowElem<T>::Chunk;
+  constexpr int E = opl::RowElem<T>::kPerChunk;
+  const int segments = gridDim.x;
+  const float* pr = partials + static_cast<std::size_t>(blockIdx.y) * segments;
+  const int lane = threadIdx.x % opl::kWaveSize;
+  float ps = 0.0f;
+  for (int i = lane; i < segments; i += opl::kWaveSize) ps += pr[i];
+  const float inv = rsqrtf(opl::wave_reduce<opl::SumOp>(ps) / static_cast<float>(cols) + epsilon);
+
+  const int c0 = blockIdx.x * seg_len;
+  const int n = min(cols - c0, seg_len);
+  const std::size_t offset = static_cast<std::size_t>(blockIdx.y) * cols + c0;
+  const T* p = input + offset;
+  const T* w = weight + c0;
+  T* o = output + offset;
+  const int t = threadIdx.x;
+  if constexpr (kChunks) {
+    const opl::Segment<T> sg(p, n);
+    const Chunk* body = reinterpret_cast<const Chunk*>(p + sg.head);
+    Chunk* obody = reinterpret_cast<Chunk*>(o + sg.head);
+    const T* wb = w + sg.head;
+    const bool w_chunks = opl::aligned16(wb);  // uniform
+    for (int i0 = t; i0 < sg.body; i0 += kSplitThreads * kSplitUnroll) {
+      Chunk q[kSplitUnroll], wq[kSplitUnroll];
+#pragma unroll
+      for (int u = 0; u < kSplitUnroll; ++u) {
+        const int i = i0 + u * kSplitThreads;
+        const int ic = i < sg.body ? i : i0;
+        q[u] = __builtin_nontemporal_load(body + ic);
+        if (w_chunks) {
+          wq[u] = reinterpret_cast<const Chunk*>(wb)[ic];
+        } else {
+#pragma unroll
+          for (int e = 0; e < E; ++e) wq[u][e] = wb[E * ic + e];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kSplitUnroll; ++u) {
+        const int i = i0 + u * kSplitThreads;
+        if (i < sg.body) {
+          Chunk y;
+#pragma unroll
+          for (int e = 0; e < E; ++e)
+            y[e] = static_cast<T>((static_cast<float>(q[u][e]) * inv) *
+                                  static_cast<float>(wq[u][e]));
+          __builtin_nontemporal_store(y, obody + i);
+        }
+      }
+    }
+    const int xc = sg.extra(t);
+    if (xc >= 0)
+      o[xc] = static_cast<T>((static_cast<float>(p[xc]) * inv) * static_cast<float>(w[xc]));
+  } else {
+    constexpr int U = 2 * kSplitUnroll;
+    for (int i0 = t; i0 < n; i0 += kSplitThreads * U) {
+      T q[U], wq[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kSplitThreads;
+        const int ic = i < n ? i : i0;
+        q[u] = __builtin_nontemporal_load(p + ic);
+        wq[u] = w[ic];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kSplitThreads;
+        if (i < n)
+          __builtin_nontemporal_store(
+              static_cast<T>((static_cast<float>(q[u]) * inv) * static_cast<float>(wq[u])), o + i);
+      }
+    }
+  }
+}
+
+inline std::size_t split_bytes(int rows, const opl::SplitPlan& p) {
+  return p.segments > 0 ? sizeof(float) * static_cast<std::size_t>(rows) * p.segments : 0;
 }
 
 template <typename T>
@@ -246,7 +424,7 @@ void launch_block(int v, const Args<T>& a, hipStream_t stream) {
 // Shared dispatch of the fp32 and fp16 entry points (E elements per 16-byte
 // chunk; per-thread counts as in softmax).
 template <typename T>
-int rmsnorm_launch(const Args<T>& args, hipStream_t stream) {
+int rmsnorm_launch(const Args<T>& args, const opl::ScratchSource& src, hipStream_t stream) {
   constexpr int E = opl::RowElem<T>::kPerChunk;
   constexpr int kWaveMaxV = opl::kRowWaveMaxCols / (opl::kWaveSize * E);
   constexpr int kBlockMinV =
@@ -254,8 +432,41 @@ int rmsnorm_launch(const Args<T>& args, hipStream_t stream) {
   constexpr int kBlockMaxV =
       opl::kRowBlockMaxCols / (opl::kRowBlockThreads * E);
   const int hidden = args.cols;
+  const opl::SplitPlan split = opl::split_plan(args.rows, hidden);
+  const std::size_t bytes = split_bytes(args.rows, split);
+  if (src.workspace_mode && !opl::workspace_ok(src.data, src.bytes, bytes))
+    return hipErrorInvalidValue;
+  if (split.segments > 0) {
+    // 4 bytes per (row, segment): fewer than 2 * kSplitTargetBlocks for
+    // split rows, one per row otherwise; every plan fits the arena.
+    opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
+    if (lease.status() != hipSuccess) return lease.status();
+    float* partials = static_cast<float*>(lease.data());
+    const dim3 grid(static_cast<unsigned>(split.segments), static_cast<unsigned>(args.rows));
+    rmsnorm_split_stats_kernel<T><<<grid, dim3(kSplitThreads), 0, stream>>>(
+        args.input, partials, hidden, split.seg_len);
+    const hipError_t status = hipGetLastError();
+    if (status != hipSuccess) return status;
+    if (opl::same_phase16(args.input, args.output))
+      return lease.launch_last(rmsnorm_split_apply_kernel<T, true>, grid, dim3(kSplitThreads),
+                               args.input, args.weight, args.output, partials, hidden,
+                               split.seg_len, args.epsilon);
+    return lease.launch_last(rmsnorm_split_apply_kernel<T, false>, grid, dim3(kSplitThreads),
+                             args.input, args.weight, args.output, partials, hidden,
+                             split.seg_len, args.epsilon);
+  }
   const bool vec = hidden % E == 0 && opl::aligned16(args.input) &&
                    opl::aligned16(args.weight) && opl::aligned16(args.output);
+  if (vec && hidden <= 32 * E) {
+    launch_group<T, E, 4>(opl::next_pow2(hidden / E), args.input, args.weight, args.output,
+                          args.rows, hidden, args.epsilon, stream);
+    return hipGetLastError();
+  }
+  if (!vec && hidden <= 32) {
+    launch_group<T, 1, 8>(opl::next_pow2(hidden), args.input, args.weight, args.output,
+                          args.rows, hidden, args.epsilon, stream);
+    return hipGetLastError();
+  }
   const bool ragged =
       !vec && opl::same_phase16(args.input, args.output) &&
       hidden >= opl::RaggedRowSlice<1, opl::kWaveSize, T>::kMinCols;
@@ -271,12 +482,8 @@ int rmsnorm_launch(const Args<T>& args, hipStream_t stream) {
       else if (ragged) launch_block<T, 0, kBlockMinV, kBlockMaxV>(plan.per_thread, args, stream);
       else launch_block<T, 1, 16, 64>(plan.per_thread, args, stream);
       break;
-    case opl::RowPath::kTwoPass:
-      rmsnorm_two_pass_kernel<T><<<dim3(args.rows), dim3(opl::kRowBlockThreads),
-                                   0, stream>>>(args.input, args.weight,
-                                                args.output, hidden,
-                                                args.epsilon);
-      break;
+    case opl::RowPath::kTwoPass:  // opl::split_plan takes every such row
+      return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -289,7 +496,7 @@ extern "C" int operatorlib_rmsnorm_f32(const float* input, const float* weight,
   if (!opl::rmsnorm_args_ok(input, weight, output, tokens, hidden, epsilon))
     return hipErrorInvalidValue;
   return rmsnorm_launch(
-      Args<float>{input, weight, output, tokens, hidden, epsilon},
+      Args<float>{input, weight, output, tokens, hidden, epsilon}, opl::ScratchSource{},
       static_cast<hipStream_t>(stream_handle));
 }
 
@@ -305,5 +512,40 @@ extern "C" int operatorlib_rmsnorm_f16(const operatorlib_half_t* input,
                      reinterpret_cast<const _Float16*>(weight),
                      reinterpret_cast<_Float16*>(output), tokens, hidden,
                      epsilon},
+      opl::ScratchSource{}, static_cast<hipStream_t>(stream_handle));
+}
+
+extern "C" size_t operatorlib_rmsnorm_f32_workspace_size(int tokens, int hidden) {
+  if (tokens <= 0 || hidden <= 0) return 0;
+  return split_bytes(tokens, opl::split_plan(tokens, hidden));
+}
+
+extern "C" int operatorlib_rmsnorm_f32_ws(const float* input, const float* weight,
+                                          float* output, int tokens, int hidden,
+                                          float epsilon, void* workspace,
+                                          size_t workspace_bytes, void* stream_handle) {
+  if (!opl::rmsnorm_args_ok(input, weight, output, tokens, hidden, epsilon))
+    return hipErrorInvalidValue;
+  return rmsnorm_launch(Args<float>{input, weight, output, tokens, hidden, epsilon},
+                        opl::ScratchSource{true, workspace, workspace_bytes},
+                        static_cast<hipStream_t>(stream_handle));
+}
+
+extern "C" size_t operatorlib_rmsnorm_f16_workspace_size(int tokens, int hidden) {
+  return operatorlib_rmsnorm_f32_workspace_size(tokens, hidden);
+}
+
+extern "C" int operatorlib_rmsnorm_f16_ws(const operatorlib_half_t* input,
+                                          const operatorlib_half_t* weight,
+                                          operatorlib_half_t* output, int tokens, int hidden,
+                                          float epsilon, void* workspace,
+                                          size_t workspace_bytes, void* stream_handle) {
+  if (!opl::rmsnorm_args_ok(input, weight, output, tokens, hidden, epsilon))
+    return hipErrorInvalidValue;
+  return rmsnorm_launch(
+      Args<_Float16>{reinterpret_cast<const _Float16*>(input),
+                     reinterpret_cast<const _Float16*>(weight),
+                     reinterpret_cast<_Float16*>(output), tokens, hidden, epsilon},
+      opl::ScratchSource{true, workspace, workspace_bytes},
       static_cast<hipStream_t>(stream_handle));
 }

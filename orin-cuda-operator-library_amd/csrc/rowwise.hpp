@@ -239,6 +239,94 @@ struct SliceFor<V, Lanes, 0, T> {
   using type = RaggedRowSlice<V, Lanes, T>;
 };
 
+// Short-row kernels: groups of G lanes per row, one access of W elements
+// per lane (W = E: a 16-byte chunk, W = 1: one element), workgroups of
+// kGroupThreads striding over blocks of rows.
+constexpr int kGroupThreads = 256;
+constexpr int kGroupMaxBlocks = 2048;
+
+template <typename T, int W>
+struct Access {
+  using type = typename RowElem<T>::Chunk;
+};
+template <typename T>
+struct Access<T, 1> {
+  typedef T type __attribute__((ext_vector_type(1)));
+};
+
+// All-reduce over aligned groups of G lanes of a wavefront (G = 1, 2, 4, 8,
+// 16 or 32): every lane of a group receives the group's value. These are
+// wave_reduce's first log2(G) butterfly steps, so the bits are the same in
+// every lane of a group; all 64 lanes must be active.
+template <class Op, int G>
+__device__ __forceinline__ float group_reduce(float v) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32, "group size");
+  if constexpr (G >= 2) v = Op::apply(v, dpp_f32<kDppQuadXor1>(v));
+  if constexpr (G >= 4) v = Op::apply(v, dpp_f32<kDppQuadXor2>(v));
+  if constexpr (G >= 8) v = Op::apply(v, dpp_f32<kDppRowHalfMirror>(v));
+  if constexpr (G >= 16) v = Op::apply(v, dpp_f32<kDppRowMirror>(v));
+  if constexpr (G >= 32) v = combine_xor16_f32<Op>(v);
+  return v;
+}
+
+// n elements from p (a segment of a row, at any element alignment) walked
+// with 16-byte accesses: `head` elements up to the first 16-byte boundary,
+// `body` aligned chunks of E elements, then `tail` (< E) elements.
+template <typename T>
+struct Segment {
+  static constexpr int kE = RowElem<T>::kPerChunk;
+  int head, body, tail;
+  __device__ __forceinline__ Segment(const T* p, int n) {
+    head = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / sizeof(T));
+    if (head > n) head = n;
+    body = (n - head) / kE;
+    tail = n - head - kE * body;
+  }
+  // The element outside the body that thread t handles, or -1: threads
+  // 0 .. head-1 the head, threads E .. E+tail-1 the tail.
+  __device__ __forceinline__ int extra(int t) const {
+    if (t < head) return t;
+    if (t >= kE && t - kE < tail) return head + kE * body + (t - kE);
+    return -1;
+  }
+};
+
+// Rows over several workgroups (softmax, RMSNorm): a row is cut into
+// `segments` segments of seg_len elements, one kSplitThreads workgroup
+// each; pass 1 writes a per-segment partial to scratch, pass 2 combines the
+// row's partials in segment order and re-reads its segment. Every row
+// longer than kRowBlockMaxCols (too long for registers) takes this path,
+// in as many segments as fill kSplitTargetBlocks workgroups (one when there
+// are that many rows); register-resident rows of a workgroup (kRowWaveMaxCols
+// < cols <= kRowBlockMaxCols) only when there are fewer than kSplitMaxRows
+// of them, which would leave most CUs idle.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitWaves = kSplitThreads / kWaveSize;
+constexpr int kSplitUnroll = 4;          // 16-byte chunks in flight per thread
+constexpr int kSplitTargetBlocks = 512;  // two workgroups per CU of a 256-CU MI355X
+constexpr int kSplitMinSegment = 2048;   // elements
+constexpr int kSplitMaxRows = 64;
+
+struct SplitPlan {
+  int segments = 0;  // 0: not split
+  int seg_len = 0;   // elements, a multiple of 64
+};
+
+inline SplitPlan split_plan(int rows, int cols) {
+  SplitPlan p;
+  if (cols <= kRowWaveMaxCols) return p;
+  const bool long_rows = cols > kRowBlockMaxCols;
+  if (!long_rows && rows >= kSplitMaxRows) return p;
+  const int by_rows = (kSplitTargetBlocks + rows - 1) / rows;
+  const int by_cols = cols / kSplitMinSegment;
+  const int want = by_rows < by_cols ? by_rows : by_cols;
+  if (want < (long_rows ? 1 : 2)) return p;
+  const int per = (cols + want - 1) / want;
+  p.seg_len = (per + 63) / 64 * 64;
+  p.segments = (cols + p.seg_len - 1) / p.seg_len;
+  return p;
+}
+
 // Same offset modulo 16 bytes.
 inline bool same_phase16(const void* a, const void* b) {
   return ((reinterpret_cast<uintptr_t>(a) ^ reinterpret_cast<uintptr_t>(b)) & 15) == 0;

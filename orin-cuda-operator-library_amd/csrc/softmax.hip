@@ -14,8 +14,10 @@
 // steps, so every path up to 32768 columns reads x once and writes once
 // (the HBM minimum: 8 bytes per fp32 element, 4 per fp16). Reductions are
 // wave64 DPP butterflies (plus an 8-slot LDS combine for workgroup rows).
-// Rows longer than 32768 columns use an online (max, sum) first pass and
-// re-read x once.
+// Rows longer than 32768 columns, and a few long rows that would leave CUs
+// idle, are cut into segments over workgroups: an online (max, sum) pass
+// per segment, then a pass that combines the row's pairs, re-reads x once
+// and writes.
 // Padding slots hold -inf, which exp maps to 0.
 
 #include <hip/hip_runtime.h>
@@ -29,6 +31,7 @@
 #include "common.hpp"
 #include "operatorlib/operatorlib_c.h"
 #include "rowwise.hpp"
+#include "scratch.hpp"
 #include "validate.hpp"
 
 namespace {
@@ -90,68 +93,6 @@ __global__ __launch_bounds__(opl::kRowBlockThreads) void softmax_block_kernel(
       exp_shift_sum(s.x, m), sum_slots);
   scale(s.x, 1.0f / sum);
   s.store(output + offset, cols, threadIdx.x);
-}
-
-// Online (running max, rescaled running sum) update for one element.
-__device__ __forceinline__ void online_update(float x, float& m, float& s) {
-  if (x > m) {
-    s = s * opl::fast_exp2((m - x) * kLog2e) + 1.0f;
-    m = x;
-  } else {
-    s += opl::fast_exp2((x - m) * kLog2e);
-  }
-}
-
-// Rows longer than the register slices: pass 1 keeps an online (max, sum)
-// per thread, pass 2 re-reads the row and writes exp(x - max) / sum.
-// `vec` selects 16-byte chunk accesses (cols % E == 0, aligned rows).
-template <typename T>
-__global__ __launch_bounds__(opl::kRowBlockThreads) void softmax_two_pass_kernel(
-    const T* __restrict__ input, T* __restrict__ output, int cols, int vec) {
-  using Chunk = typename opl::RowElem<T>::Chunk;
-  constexpr int E = opl::RowElem<T>::kPerChunk;
-  __shared__ float max_slots[opl::kRowBlockWaves];
-  __shared__ float sum_slots[opl::kRowBlockWaves];
-  const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols;
-  const T* row = input + offset;
-  T* out = output + offset;
-  const int t = threadIdx.x;
-  constexpr int kT = opl::kRowBlockThreads;
-  float m = -FLT_MAX;
-  float s = 0.0f;
-  if (vec) {
-    const Chunk* rc = reinterpret_cast<const Chunk*>(row);
-    for (int i = t; i < cols / E; i += kT) {
-      const Chunk q = rc[i];
-#pragma unroll
-      for (int e = 0; e < E; ++e) online_update(static_cast<float>(q[e]), m, s);
-    }
-  } else {
-    for (int c = t; c < cols; c += kT)
-      online_update(static_cast<float>(row[c]), m, s);
-  }
-  const float row_max =
-      opl::block_reduce<opl::MaxOp, opl::kRowBlockWaves>(m, max_slots);
-  const float row_sum = opl::block_reduce<opl::SumOp, opl::kRowBlockWaves>(
-      s * opl::fast_exp2((m - row_max) * kLog2e), sum_slots);
-  const float inv = 1.0f / row_sum;
-  if (vec) {
-    const Chunk* rc = reinterpret_cast<const Chunk*>(row);
-    Chunk* oc = reinterpret_cast<Chunk*>(out);
-    for (int i = t; i < cols / E; i += kT) {
-      const Chunk q = rc[i];
-      Chunk y;
-#pragma unroll
-      for (int e = 0; e < E; ++e)
-        y[e] = static_cast<T>(
-            opl::fast_exp2((static_cast<float>(q[e]) - row_max) * kLog2e) * inv);
-      oc[i] = y;
-    }
-  } else {
-    for (int c = t; c < cols; c += kT)
-      out[c] = static_cast<T>(
-          opl::fast_exp2((static_cast<float>(row[c]) - row_max) * kLog2e) * inv);
-  }
 }
 
 // Ragged fp32 rows of up to kTileMaxCols columns (cols % 4 != 0 or
@@ -253,6 +194,208 @@ void launch_tile(int v, const float* in, float* out, int rows, int cols,
       in, out, rows, cols);
 }
 
+// Short rows: a group of G lanes per row, 64 / G rows per wavefront, one
+// access per lane: W = E (16-byte chunk t of the row; cols % E == 0 and
+// aligned rows) or W = 1 (element t, any shape). A wavefront per row left
+// most lanes idle here (1048576 x 8: 135 us against a 10 us copy of the
+// same bytes). Wavefronts stride over blocks of rows, U blocks in flight.
+using opl::kGroupMaxBlocks;
+using opl::kGroupThreads;
+
+template <typename T, int G, int W, int U>
+__global__ __launch_bounds__(kGroupThreads) void softmax_group_kernel(
+    const T* __restrict__ input, T* __restrict__ output, int rows, int cols) {
+  using A = typename opl::Access<T, W>::type;
+  constexpr int kRowsPerWave = opl::kWaveSize / G;
+  constexpr int kWaves = kGroupThreads / opl::kWaveSize;
+  const int lane = threadIdx.x % opl::kWaveSize;
+  const int t = lane % G;
+  const int r_lane = lane / G;
+  const bool lane_in = t * W < cols;
+  const long long stride = static_cast<long long>(gridDim.x) * kWaves * kRowsPerWave * U;
+  for (long long r0 = (static_cast<long long>(blockIdx.x) * kWaves + threadIdx.x / opl::kWaveSize) *
+                      kRowsPerWave * U;
+       r0 < rows; r0 += stride) {
+    A q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long row = r0 + u * kRowsPerWave + r_lane;
+      const bool in = lane_in && row < rows;
+      q[u] = __builtin_nontemporal_load(
+          reinterpret_cast<const A*>(input + (in ? row * cols + t * W : 0)));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long row = r0 + u * kRowsPerWave + r_lane;
+      const bool in = lane_in && row < rows;
+      float x[W];
+#pragma unroll
+      for (int e = 0; e < W; ++e) x[e] = in ? static_cast<float>(q[u][e]) : -INFINITY;
+      const float m = opl::group_reduce<opl::MaxOp, G>(local_max(x));
+      const float inv = 1.0f / opl::group_reduce<opl::SumOp, G>(exp_shift_sum(x, m));
+      if (in) {
+        A y;
+#pragma unroll
+        for (int e = 0; e < W; ++e) y[e] = static_cast<T>(x[e] * inv);
+        __builtin_nontemporal_store(y, reinterpret_cast<A*>(output + row * cols + t * W));
+      }
+    }
+  }
+}
+
+template <typename T, int W, int U, int G = 1>
+void launch_group(int g, const T* in, T* out, int rows, int cols, hipStream_t stream) {
+  if constexpr (G < 32) {
+    if (g > G) return launch_group<T, W, U, 2 * G>(g, in, out, rows, cols, stream);
+  }
+  constexpr int kRowsPerBlock = kGroupThreads / G * U;
+  const long long blocks = (static_cast<long long>(rows) + kRowsPerBlock - 1) / kRowsPerBlock;
+  softmax_group_kernel<T, G, W, U>
+      <<<dim3(static_cast<unsigned>(blocks < kGroupMaxBlocks ? blocks : kGroupMaxBlocks)),
+         dim3(kGroupThreads), 0, stream>>>(in, out, rows, cols);
+}
+
+// Rows over several workgroups (opl::split_plan picks them: rows too long
+// for registers, and few long rows, where one workgroup per row left most
+// CUs idle: 32 x 50257 took 34.5 us, 1 x 2^20 357 us). Pass 1 writes every
+// segment's (max, sum of exp(x - max)) to scratch; pass 2 combines the
+// row's pairs in segment order (every wavefront of the row computes the
+// same bits), re-reads its segment (from the caches at these sizes) and
+// writes exp(x - max) / sum. Segments walk their elements with 16-byte
+// accesses at any alignment (opl::Segment).
+using opl::kSplitThreads;
+using opl::kSplitUnroll;
+using opl::kSplitWaves;
+using opl::SplitPlan;
+
+inline std::size_t split_bytes(int rows, const SplitPlan& p) {
+  return p.segments > 0 ? sizeof(float2) * static_cast<std::size_t>(rows) * p.segments : 0;
+}
+
+// (m, s) <- running max and sum of exp(x - m) after the values x[0..N).
+template <int N>
+__device__ __forceinline__ void online_block(const float (&x)[N], float& m, float& s) {
+  const float nm = fmaxf(m, local_max(x));
+  s *= opl::fast_exp2((m - nm) * kLog2e);
+#pragma unroll
+  for (int e = 0; e < N; ++e) s += opl::fast_exp2((x[e] - nm) * kLog2e);
+  m = nm;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void softmax_split_stats_kernel(
+    const T* __restrict__ input, float2* __restrict__ partials, int cols, int seg_len) {
+  using Chunk = typename opl::RowElem<T>::Chunk;
+  constexpr int E = opl::RowElem<T>::kPerChunk;
+  __shared__ float max_slots[kSplitWaves];
+  __shared__ float sum_slots[kSplitWaves];
+  const int c0 = blockIdx.x * seg_len;
+  const int n = min(cols - c0, seg_len);
+  const T* p = input + static_cast<std::size_t>(blockIdx.y) * cols + c0;
+  const opl::Segment<T> sg(p, n);
+  const Chunk* body = reinterpret_cast<const Chunk*>(p + sg.head);
+  const int t = threadIdx.x;
+  // -FLT_MAX, not -inf: a thread with no elements, or only -inf ones,
+  // keeps s = 0 through every rescale.
+  float m = -FLT_MAX, s = 0.0f;
+  for (int i0 = t; i0 < sg.body; i0 += kSplitThreads * kSplitUnroll) {
+    Chunk q[kSplitUnroll];
+#pragma unroll
+    for (int u = 0; u < kSplitUnroll; ++u) {
+      const int i = i0 + u * kSplitThreads;
+      q[u] = body[i < sg.body ? i : i0];  // cached: pass 2 reads it again
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitUnroll; ++u) {
+      if (i0 + u * kSplitThreads < sg.body) {
+        float x[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = static_cast<float>(q[u][e]);
+        online_block(x, m, s);
+      }
+    }
+  }
+  const int xc = sg.extra(t);
+  if (xc >= 0) {
+    const float x[1] = {static_cast<float>(p[xc])};
+    online_block(x, m, s);
+  }
+  const float seg_max = opl::block_reduce<opl::MaxOp, kSplitWaves>(m, max_slots);
+  const float seg_sum = opl::block_reduce<opl::SumOp, kSplitWaves>(
+      s * opl::fast_exp2((m - seg_max) * kLog2e), sum_slots);
+  if (t == 0)
+    partials[static_cast<std::size_t>(blockIdx.y) * gridDim.x + blockIdx.x] =
+        make_float2(seg_max, seg_sum);
+}
+
+// kChunks: input and output rows share their 16-byte phase (16-byte
+// accesses on both sides); otherwise element accesses.
+template <typename T, bool kChunks>
+__global__ __launch_bounds__(kSplitThreads) void softmax_split_apply_kernel(
+    const T* __restrict__ input, T* __restrict__ output,
+    const float2* __restrict__ partials, int cols, int seg_len) {
+  using Chunk = typename opl::RowElem<T>::Chunk;
+  constexpr int E = opl::RowElem<T>::kPerChunk;
+  const int segments = gridDim.x;
+  const float2* pr = partials + static_cast<std::size_t>(blockIdx.y) * segments;
+  const int lane = threadIdx.x % opl::kWaveSize;
+  float pm = -FLT_MAX;
+  for (int i = lane; i < segments; i += opl::kWaveSize) pm = fmaxf(pm, pr[i].x);
+  const float row_max = opl::wave_reduce<opl::MaxOp>(pm);
+  float ps = 0.0f;
+  for (int i = lane; i < segments; i += opl::kWaveSize)
+    ps += pr[i].y * opl::fast_exp2((pr[i].x - row_max) * kLog2e);
+  const float inv = 1.0f / opl::wave_reduce<opl::SumOp>(ps);
+  auto f = [&](float x) { return opl::fast_exp2((x - row_max) * kLog2e) * inv; };
+
+  const int c0 = blockIdx.x * seg_len;
+  const int n = min(cols - c0, seg_len);
+  const std::size_t offset = static_cast<std::size_t>(blockIdx.y) * cols + c0;
+  const T* p = input + offset;
+  T* o = output + offset;
+  const int t = threadIdx.x;
+  if constexpr (kChunks) {
+    const opl::Segment<T> sg(p, n);
+    const Chunk* body = reinterpret_cast<const Chunk*>(p + sg.head);
+    Chunk* obody = reinterpret_cast<Chunk*>(o + sg.head);
+    for (int i0 = t; i0 < sg.body; i0 += kSplitThreads * kSplitUnroll) {
+      Chunk q[kSplitUnroll];
+#pragma unroll
+      for (int u = 0; u < kSplitUnroll; ++u) {
+        const int i = i0 + u * kSplitThreads;
+        q[u] = __builtin_nontemporal_load(body + (i < sg.body ? i : i0));
+      }
+#pragma unroll
+      for (int u = 0; u < kSplitUnroll; ++u) {
+        const int i = i0 + u * kSplitThreads;
+        if (i < sg.body) {
+          Chunk y;
+#pragma unroll
+          for (int e = 0; e < E; ++e) y[e] = static_cast<T>(f(static_cast<float>(q[u][e])));
+          __builtin_nontemporal_store(y, obody + i);
+        }
+      }
+    }
+    const int xc = sg.extra(t);
+    if (xc >= 0) o[xc] = static_cast<T>(f(static_cast<float>(p[xc])));
+  } else {
+    constexpr int U = 2 * kSplitUnroll;
+    for (int i0 = t; i0 < n; i0 += kSplitThreads * U) {
+      T q[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kSplitThreads;
+        q[u] = __builtin_nontemporal_load(p + (i < n ? i : i0));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kSplitThreads;
+        if (i < n) __builtin_nontemporal_store(static_cast<T>(f(static_cast<float>(q[u]))), o + i);
+      }
+    }
+  }
+}
+
 // Launches the kernel instance whose per-thread count V is the smallest power
 // of two >= v (v comes from pick_row_plan, so it never exceeds MaxV).
 template <typename T, int W, int V, int MaxV>
@@ -283,15 +426,45 @@ void launch_block(int v, const T* in, T* out, int rows, int cols,
 // register budget (64 fp32 values per thread).
 template <typename T>
 int softmax_launch(const T* input, T* output, int rows, int cols,
-                   hipStream_t stream) {
+                   const opl::ScratchSource& src, hipStream_t stream) {
   constexpr int E = opl::RowElem<T>::kPerChunk;
   constexpr int kWaveMaxV = opl::kRowWaveMaxCols / (opl::kWaveSize * E);
   constexpr int kBlockMinV =
       2 * opl::kRowWaveMaxCols / (opl::kRowBlockThreads * E);
   constexpr int kBlockMaxV =
       opl::kRowBlockMaxCols / (opl::kRowBlockThreads * E);
+  const SplitPlan split = opl::split_plan(rows, cols);
+  const std::size_t bytes = split_bytes(rows, split);
+  if (src.workspace_mode && !opl::workspace_ok(src.data, src.bytes, bytes))
+    return hipErrorInvalidValue;
+  if (split.segments > 0) {
+    // 8 bytes per (row, segment): fewer than 2 * kSplitTargetBlocks pairs
+    // for split rows, one per row otherwise (a matrix that fits in HBM has
+    // far fewer rows than the arena holds pairs).
+    opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
+    if (lease.status() != hipSuccess) return lease.status();
+    float2* partials = static_cast<float2*>(lease.data());
+    const dim3 grid(static_cast<unsigned>(split.segments), static_cast<unsigned>(rows));
+    softmax_split_stats_kernel<T><<<grid, dim3(kSplitThreads), 0, stream>>>(
+        input, partials, cols, split.seg_len);
+    const hipError_t status = hipGetLastError();
+    if (status != hipSuccess) return status;
+    if (opl::same_phase16(input, output))
+      return lease.launch_last(softmax_split_apply_kernel<T, true>, grid, dim3(kSplitThreads),
+                               input, output, partials, cols, split.seg_len);
+    return lease.launch_last(softmax_split_apply_kernel<T, false>, grid, dim3(kSplitThreads),
+                             input, output, partials, cols, split.seg_len);
+  }
   const bool vec =
       cols % E == 0 && opl::aligned16(input) && opl::aligned16(output);
+  if (vec && cols <= 32 * E) {
+    launch_group<T, E, 4>(opl::next_pow2(cols / E), input, output, rows, cols, stream);
+    return hipGetLastError();
+  }
+  if (!vec && cols <= 32) {
+    launch_group<T, 1, 8>(opl::next_pow2(cols), input, output, rows, cols, stream);
+    return hipGetLastError();
+  }
   // Ragged rows (cols % E != 0 or unaligned) keep 16-byte accesses when
   // input and output rows share their 16-byte phase.
   const bool ragged =
@@ -312,10 +485,8 @@ int softmax_launch(const T* input, T* output, int rows, int cols,
       else if (ragged) launch_block<T, 0, kBlockMinV, kBlockMaxV>(plan.per_thread, input, output, rows, cols, stream);
       else launch_block<T, 1, 16, 64>(plan.per_thread, input, output, rows, cols, stream);
       break;
-    case opl::RowPath::kTwoPass:
-      softmax_two_pass_kernel<T><<<dim3(rows), dim3(opl::kRowBlockThreads), 0,
-                                   stream>>>(input, output, cols, vec ? 1 : 0);
-      break;
+    case opl::RowPath::kTwoPass:  // split_plan takes every such row
+      return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -327,7 +498,7 @@ extern "C" int operatorlib_softmax_f32(const float* input, float* output,
                                        void* stream_handle) {
   if (!opl::matrix_args_ok(input, output, rows, cols))
     return hipErrorInvalidValue;
-  return softmax_launch(input, output, rows, cols,
+  return softmax_launch(input, output, rows, cols, opl::ScratchSource{},
                         static_cast<hipStream_t>(stream_handle));
 }
 
@@ -338,5 +509,36 @@ extern "C" int operatorlib_softmax_f16(const operatorlib_half_t* input,
     return hipErrorInvalidValue;
   return softmax_launch(reinterpret_cast<const _Float16*>(input),
                         reinterpret_cast<_Float16*>(output), rows, cols,
+                        opl::ScratchSource{}, static_cast<hipStream_t>(stream_handle));
+}
+
+extern "C" size_t operatorlib_softmax_f32_workspace_size(int rows, int cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return split_bytes(rows, opl::split_plan(rows, cols));
+}
+
+extern "C" int operatorlib_softmax_f32_ws(const float* input, float* output, int rows,
+                                          int cols, void* workspace, size_t workspace_bytes,
+                                          void* stream_handle) {
+  if (!opl::matrix_args_ok(input, output, rows, cols))
+    return hipErrorInvalidValue;
+  return softmax_launch(input, output, rows, cols,
+                        opl::ScratchSource{true, workspace, workspace_bytes},
+                        static_cast<hipStream_t>(stream_handle));
+}
+
+extern "C" size_t operatorlib_softmax_f16_workspace_size(int rows, int cols) {
+  return operatorlib_softmax_f32_workspace_size(rows, cols);
+}
+
+extern "C" int operatorlib_softmax_f16_ws(const operatorlib_half_t* input,
+                                          operatorlib_half_t* output, int rows, int cols,
+                                          void* workspace, size_t workspace_bytes,
+                                          void* stream_handle) {
+  if (!opl::matrix_args_ok(input, output, rows, cols))
+    return hipErrorInvalidValue;
+  return softmax_launch(reinterpret_cast<const _Float16*>(input),
+                        reinterpret_cast<_Float16*>(output), rows, cols,
+                        opl::ScratchSource{true, workspace, workspace_bytes},
                         static_cast<hipStream_t>(stream_handle));
 }

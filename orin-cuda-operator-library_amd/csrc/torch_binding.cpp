@@ -155,13 +155,15 @@ at::Tensor softmax_op(const at::Tensor& input) {
   const auto [rows, cols] = rows_by_last(in, input, "last dimension");
   at::Tensor out = at::empty_like(input);
   launch(in, [&](void* s) {
+    const Workspace ws(in, operatorlib_softmax_f32_workspace_size(rows, cols));
     return in.half()
-               ? operatorlib_softmax_f16(
+               ? operatorlib_softmax_f16_ws(
                      static_cast<const operatorlib_half_t*>(caddr(input)),
-                     static_cast<operatorlib_half_t*>(out.data_ptr()), rows, cols, s)
-               : operatorlib_softmax_f32(static_cast<const float*>(caddr(input)),
-                                         static_cast<float*>(out.data_ptr()), rows,
-                                         cols, s);
+                     static_cast<operatorlib_half_t*>(out.data_ptr()), rows, cols,
+                     ws.data(), ws.bytes(), s)
+               : operatorlib_softmax_f32_ws(static_cast<const float*>(caddr(input)),
+                                            static_cast<float*>(out.data_ptr()), rows,
+                                            cols, ws.data(), ws.bytes(), s);
   });
   return out;
 }
@@ -192,16 +194,17 @@ at::Tensor rmsnorm_op(const at::Tensor& input, const at::Tensor& weight,
   const float eps = static_cast<float>(epsilon);
   at::Tensor out = at::empty_like(input);
   launch(in, [&](void* s) {
+    const Workspace ws(in, operatorlib_rmsnorm_f32_workspace_size(tokens, hidden));
     return in.half()
-               ? operatorlib_rmsnorm_f16(
+               ? operatorlib_rmsnorm_f16_ws(
                      static_cast<const operatorlib_half_t*>(caddr(input)),
                      static_cast<const operatorlib_half_t*>(caddr(weight)),
                      static_cast<operatorlib_half_t*>(out.data_ptr()), tokens, hidden,
-                     eps, s)
-               : operatorlib_rmsnorm_f32(static_cast<const float*>(caddr(input)),
-                                         static_cast<const float*>(caddr(weight)),
-                                         static_cast<float*>(out.data_ptr()), tokens,
-                                         hidden, eps, s);
+                     eps, ws.data(), ws.bytes(), s)
+               : operatorlib_rmsnorm_f32_ws(static_cast<const float*>(caddr(input)),
+                                            static_cast<const float*>(caddr(weight)),
+                                            static_cast<float*>(out.data_ptr()), tokens,
+                                            hidden, eps, ws.data(), ws.bytes(), s);
   });
   return out;
 }

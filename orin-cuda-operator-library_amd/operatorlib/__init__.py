@@ -63,6 +63,20 @@ C_SYMBOLS = {
     "operatorlib_reduce_sum_f32_workspace_size": (_c.c_size_t, [_c.c_void_p, _c.c_size_t]),
     "operatorlib_reduce_sum_f32_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_size_t,
                                                  _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "operatorlib_softmax_f32_workspace_size": (_c.c_size_t, [_c.c_int, _c.c_int]),
+    "operatorlib_softmax_f32_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int,
+                                              _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "operatorlib_softmax_f16_workspace_size": (_c.c_size_t, [_c.c_int, _c.c_int]),
+    "operatorlib_softmax_f16_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int,
+                                              _c.c_void_p, _c.c_size_t, _c.c_void_p]),
+    "operatorlib_rmsnorm_f32_workspace_size": (_c.c_size_t, [_c.c_int, _c.c_int]),
+    "operatorlib_rmsnorm_f32_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int,
+                                              _c.c_int, _c.c_float, _c.c_void_p, _c.c_size_t,
+                                              _c.c_void_p]),
+    "operatorlib_rmsnorm_f16_workspace_size": (_c.c_size_t, [_c.c_int, _c.c_int]),
+    "operatorlib_rmsnorm_f16_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int,
+                                              _c.c_int, _c.c_float, _c.c_void_p, _c.c_size_t,
+                                              _c.c_void_p]),
     "operatorlib_gemm_f32_workspace_size": (_c.c_size_t, [_c.c_void_p, _c.c_void_p, _c.c_int,
                                                           _c.c_int, _c.c_int]),
     "operatorlib_gemm_f32_ws": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int,

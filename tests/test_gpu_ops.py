@@ -158,6 +158,43 @@ def test_softmax_pins(hip):
     pins.pin_softmax(hip.softmax, tol=2e-7)
 
 
+# Short rows run G lanes per row (up to 32 elements, or 32 chunks of
+# 16-byte aligned rows: vec G = 2, 4 with an idle lane, 32; element G = 1,
+# 2, 32); few long rows are split over workgroups, whose (max, sum) pairs
+# every workgroup of the row combines in segment order (two-pass rows, and
+# register-resident rows when there are fewer than 64).
+SOFTMAX_GROUP_SHAPES = [(100000, 8), (4099, 12), (3001, 128), (70001, 1), (65, 2),
+                        (20000, 31)]
+SOFTMAX_SPLIT_SHAPES = [(1, 1 << 20), (32, 50257), (63, 5000), (5, 131075), (511, 40000)]
+
+
+@pytest.mark.parametrize("shape", SOFTMAX_GROUP_SHAPES + SOFTMAX_SPLIT_SHAPES)
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_softmax_short_and_split_rows(hip, shape, offset):
+    x = oracle.normal(220 + shape[1] % 997, shape, 0.0, 3.0)
+    ref = oracle.softmax(x)
+    y = hip.softmax(x, offset)
+    elem, norm = rel_errors(y, ref)
+    assert elem <= 1e-5 and norm <= 1e-5, (elem, norm)
+
+
+@pytest.mark.parametrize("shape", [(2, 50000), (3, 9000), (700, 8), (700, 5)])
+def test_softmax_masked_rows(hip, shape):
+    # -inf everywhere but a few columns: whole segments (split rows) and
+    # whole lane groups hold only -inf, and must add nothing to the sum.
+    rows, cols = shape
+    x = np.full(shape, -np.inf, np.float32)
+    x[0, cols - 3:] = [0.5, -1.0, 2.0]
+    x[1, 1] = 3.0
+    x[2:, 0] = oracle.normal(230, rows - 2)
+    x[2:, cols - 1] = 1.0
+    ref = oracle.softmax(x)
+    y = hip.softmax(x)
+    assert np.all(np.isfinite(y))
+    assert np.max(np.abs(y - ref)) <= 1e-6
+    assert np.all(y[x == -np.inf] == 0.0)
+
+
 # Input and output in different 16-byte phases (rows cannot share one
 # float4 layout): the element-wise paths. The weight of RMSNorm may sit at
 # any alignment on every path.
@@ -282,6 +319,27 @@ def test_rmsnorm_matches_oracle(hip, shape, eps, offset):
 
 def test_rmsnorm_pins(hip):
     pins.pin_rmsnorm(hip.rmsnorm, tol=3e-7)
+
+
+# Short rows run G lanes per row; few long rows, and every row past 32768
+# columns, are split over workgroups whose partial sums of squares the row's
+# workgroups add in segment order. The weights sit at the input's offset, so
+# odd widths put most rows at another 16-byte phase than the weights.
+RMSNORM_GROUP_CASES = [((100000, 16), 1e-6), ((4099, 12), 1e-5), ((3001, 128), 1e-5),
+                       ((70001, 1), 1e-5), ((20000, 31), 1e-6)]
+RMSNORM_SPLIT_CASES = [((4, 1 << 20), 1e-6), ((64, 65536), 1e-6), ((63, 5000), 1e-5),
+                       ((600, 40003), 1e-6)]
+
+
+@pytest.mark.parametrize("shape,eps", RMSNORM_GROUP_CASES + RMSNORM_SPLIT_CASES)
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_rmsnorm_short_and_split_rows(hip, shape, eps, offset):
+    x = oracle.normal(520 + shape[1] % 997, shape)
+    w = oracle.uniform(521, shape[1], 0.5, 1.5)
+    ref = oracle.rmsnorm(x, w, eps)
+    y = hip.rmsnorm(x, w, eps, offset)
+    elem, norm = rel_errors(y, ref)
+    assert elem <= 1e-5 and norm <= 1e-5, (elem, norm)
 
 
 def test_rmsnorm_nan_epsilon_is_accepted_as_in_the_reference(lib):

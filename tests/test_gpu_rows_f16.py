@@ -78,11 +78,13 @@ def rmsnorm_f16(lib, x_bits, w_bits, eps, in_off=0, out_off=0, w_off=0) -> np.nd
 
 # Every dispatch path: 16-byte chunk rows (cols % 8 == 0), ragged rows
 # (chunk body at any 2-byte phase, cols >= 16), element rows (cols < 16 or
-# input / output in different phases), workgroup rows (> 4096) and the
-# two-pass path (> 32768).
+# input / output in different phases), workgroup rows (> 4096), lane groups
+# of short rows, and rows split over workgroups (> 32768, or few long rows).
 SHAPES = [(19, 128), (17, 1024), (17, 1003), (5, 1), (3, 7), (3, 15), (3, 16),
           (1, 4096), (7, 4100), (3, 9000), (2, 32768), (2, 40000), (3, 33333),
-          (4096, 1024), (4097, 1023), (2048, 4096), (2047, 4095)]
+          (4096, 1024), (4097, 1023), (2048, 4096), (2047, 4095),
+          # short rows in lane groups; rows split over workgroups
+          (50000, 24), (3001, 256), (1, 1 << 20), (700, 40003)]
 OFFSETS = [0, 1, 3, 7]          # elements: every 16-byte phase parity
 
 
@@ -123,7 +125,9 @@ def test_softmax_f16_constant_rows(lib):
 
 RMS_CASES = [((32, 4096), 1e-5), ((17, 1003), 1e-5), ((21, 1024), 1e-5),
              ((3, 1), 1e-5), ((3, 15), 1e-5), ((4, 10000), 1e-6), ((2, 32768), 1e-6),
-             ((2, 40001), 1e-6), ((2048, 4096), 1e-6), ((2047, 4095), 1e-6)]
+             ((2, 40001), 1e-6), ((2048, 4096), 1e-6), ((2047, 4095), 1e-6),
+             ((50000, 24), 1e-6), ((3001, 256), 1e-5), ((2, 1 << 20), 1e-6),
+             ((700, 40003), 1e-6)]
 
 
 @pytest.mark.parametrize("shape,eps", RMS_CASES)

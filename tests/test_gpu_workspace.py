@@ -7,7 +7,8 @@ is enqueued (the output keeps its NaN fill). Cases: every launch sequence
 that uses scratch (reduce partials, decode split-K partials on both skinny
 kernels, padded fp16 operands at the 4095^3 BASELINE edge shape, the split
 last round of 256 x 256-tile fp16 and fp32 grids, small grids split along
-K, split fp32 and fp16 register-staged attention).
+K, split fp32 and fp16 register-staged attention, softmax and RMSNorm rows
+split over workgroups).
 """
 
 from __future__ import annotations
@@ -61,6 +62,46 @@ def test_reduce_ws_matches_plain(lib, n):
               lambda: lib.operatorlib_reduce_sum_f32_workspace_size(ptr(x), n), out)
     ref = oracle.reduce_sum(x.cpu().numpy())
     assert abs(y.item() - ref) <= 1e-5 * abs(ref)
+
+
+# (rows, cols): few long rows split over workgroups, rows past 32768
+# columns (one segment each), and shapes that need no scratch.
+ROW_CASES = [(1, 1 << 20), (32, 50257), (63, 5000), (600, 40003), (4096, 1024), (100000, 8)]
+
+
+@pytest.mark.parametrize("rows,cols", ROW_CASES)
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_softmax_ws_matches_plain(lib, rows, cols, dtype):
+    x = oracle.normal(80, (rows, cols), 0.0, 3.0)
+    if dtype == "f16":
+        d = to_device(oracle.to_f16_bits(x))
+        out = torch.full((rows, cols), float("nan"), dtype=torch.float16, device="cuda")
+    else:
+        d, out = to_device(x), empty((rows, cols))
+    plain = getattr(lib, f"operatorlib_softmax_{dtype}")
+    ws = getattr(lib, f"operatorlib_softmax_{dtype}_ws")
+    query = getattr(lib, f"operatorlib_softmax_{dtype}_workspace_size")
+    _both(lambda s: plain(ptr(d), ptr(out), rows, cols, s),
+          lambda w, b, s: ws(ptr(d), ptr(out), rows, cols, w, b, s),
+          lambda: query(rows, cols), out)
+
+
+@pytest.mark.parametrize("rows,cols", ROW_CASES)
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_rmsnorm_ws_matches_plain(lib, rows, cols, dtype):
+    x = oracle.normal(81, (rows, cols))
+    w = oracle.uniform(82, cols, 0.5, 1.5)
+    if dtype == "f16":
+        d, dw = to_device(oracle.to_f16_bits(x)), to_device(oracle.to_f16_bits(w))
+        out = torch.full((rows, cols), float("nan"), dtype=torch.float16, device="cuda")
+    else:
+        d, dw, out = to_device(x), to_device(w), empty((rows, cols))
+    plain = getattr(lib, f"operatorlib_rmsnorm_{dtype}")
+    ws = getattr(lib, f"operatorlib_rmsnorm_{dtype}_ws")
+    query = getattr(lib, f"operatorlib_rmsnorm_{dtype}_workspace_size")
+    _both(lambda s: plain(ptr(d), ptr(dw), ptr(out), rows, cols, 1e-6, s),
+          lambda wp, b, s: ws(ptr(d), ptr(dw), ptr(out), rows, cols, 1e-6, wp, b, s),
+          lambda: query(rows, cols), out)
 
 
 # (m, n, k, dtype): narrow decode shapes (split K) on both skinny kernels,

@@ -62,7 +62,7 @@ def lib():
 
 def test_every_declared_symbol_is_exported(lib):
     names = declared_c_functions()
-    assert len(names) == 23, names
+    assert len(names) == 31, names
     assert set(names) == set(operatorlib.C_SYMBOLS)
     for name in names:
         assert hasattr(lib, name), name
@@ -228,6 +228,41 @@ def test_gemm_workspace_size(lib):
     assert f16(FAKE, FAKE, 333, 777, 999) == 0
     assert f32(FAKE, FAKE, 200, 200, 200) == 0
     assert f16(NULL, FAKE, 1, 4096, 4096) == 0  # invalid arguments
+
+
+def test_rowwise_workspace_size(lib):
+    # Rows split over workgroups: 512 target workgroups, segments of at
+    # least 2048 elements rounded up to 64; 8 bytes per (row, segment) for
+    # softmax, 4 for RMSNorm. Rows of at most 4096 columns, and 64 or more
+    # rows of at most 32768, need none; longer rows always split (one
+    # segment per row once there are 512 rows).
+    for q, pair in ((lib.operatorlib_softmax_f32_workspace_size, 8),
+                    (lib.operatorlib_softmax_f16_workspace_size, 8),
+                    (lib.operatorlib_rmsnorm_f32_workspace_size, 4),
+                    (lib.operatorlib_rmsnorm_f16_workspace_size, 4)):
+        assert q(4096, 1024) == 0
+        assert q(1 << 20, 8) == 0
+        assert q(64, 32768) == 0
+        assert q(1, 1 << 20) == pair * 512           # 512 segments of 2048
+        assert q(32, 50257) == pair * 32 * 16        # 16 segments of 3200
+        assert q(63, 5000) == pair * 63 * 2          # 2 segments of 2560
+        assert q(4, 1 << 20) == pair * 4 * 128       # 128 segments of 8192
+        assert q(600, 40000) == pair * 600           # one segment per row
+        assert q(0, 5000) == 0 and q(3, 0) == 0      # invalid sizes
+
+
+def test_rowwise_ws_reject_short_workspace(lib):
+    ws = ctypes.c_void_p(0x100000)
+    assert lib.operatorlib_softmax_f32_ws(FAKE, FAKE, 1, 1 << 20, NULL, 0, NULL) == INVALID
+    assert lib.operatorlib_softmax_f16_ws(FAKE, FAKE, 32, 50257, ws, 4095, NULL) == INVALID
+    assert lib.operatorlib_rmsnorm_f32_ws(FAKE, FAKE, FAKE, 4, 1 << 20, 1e-5, ws, 1024,
+                                          NULL) == INVALID
+    assert lib.operatorlib_rmsnorm_f16_ws(FAKE, FAKE, FAKE, 63, 5000, 1e-5,
+                                          ctypes.c_void_p(0x100000 + 16), 1 << 20,
+                                          NULL) == INVALID   # not 256-byte aligned
+    # argument checks as in the plain forms
+    assert lib.operatorlib_softmax_f32_ws(NULL, FAKE, 4, 4, NULL, 0, NULL) == INVALID
+    assert lib.operatorlib_rmsnorm_f32_ws(FAKE, FAKE, FAKE, 4, 4, 0.0, NULL, 0, NULL) == INVALID
 
 
 @pytest.mark.parametrize("bytes_given", [0, 1000])
