@@ -253,7 +253,11 @@ TRANSPOSE_SHAPES = [(37, 65), (64, 96), (65, 37), (1, 1), (1, 1000), (1000, 1),
                     (1030, 1031), (2049, 1027), (1000, 1000),
                     # ... or, at offset 0, aligned input rows and misaligned
                     # output rows (cached stores)
-                    (1027, 2048), (4097, 4096)]
+                    (1027, 2048), (4097, 4096),
+                    # at most 8 rows or columns: one thread per index of the
+                    # long side, 1 to 8 values of the short side each
+                    (1, 1 << 20), (1 << 20, 1), (3, 100003), (100003, 3),
+                    (8, 4097), (4097, 8), (7, 9), (9, 7), (2, 2)]
 
 
 @pytest.mark.parametrize("shape", TRANSPOSE_SHAPES)
