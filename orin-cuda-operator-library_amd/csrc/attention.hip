@@ -728,7 +728,7 @@ __global__ __launch_bounds__(kW * opl::kWaveSize * kGroups)
 __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd<T, D, kGroups, kW, kTileKeys>, 2)))
 void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                           const T* __restrict__ V, float* __restrict__ O, int BH, int S,
-                          int causal, float score_scale_log2) {
+                          int dm, int causal, float score_scale_log2) {
   using L = Layout<T, D, kTileKeys>;
   constexpr bool kHalf = L::kSize == 2;
   using Frag = typename std::conditional<kHalf, half8, floatx4>::type;
@@ -792,7 +792,10 @@ void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   const int col = lane % 16;
   const int quad = lane / 16;
   const int wave_row0 = q0 + wave * kRowsPerWave;
-  const std::size_t head = static_cast<std::size_t>(bh) * S * D;
+  // dm: the tensors' head dim (memory rows of dm elements); D >= dm is the
+  // LDS layout's. Dims from dm on are zeros in Q and in the K/V tiles (their
+  // products add nothing) and are not stored.
+  const std::size_t head = static_cast<std::size_t>(bh) * S * dm;
   const T* qh = Q + head;
   const T* kh = K + head;
   const T* vh = V + head;
@@ -803,44 +806,47 @@ void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
 #pragma unroll
   for (int qc = 0; qc < 2; ++qc)
 #pragma unroll
-    for (int c = 0; c < L::kSteps; ++c)
+    for (int c = 0; c < L::kSteps; ++c) {
+      const int dim = L::kSubK * c + L::kElems * quad;
       qf[qc][c] = *reinterpret_cast<const Frag*>(
-          qh + static_cast<std::size_t>(min(wave_row0 + 16 * qc + col, S - 1)) * D +
-          L::kSubK * c + L::kElems * quad);
+          qh + static_cast<std::size_t>(min(wave_row0 + 16 * qc + col, S - 1)) * dm +
+          (dim < dm ? dim : 0));
+      if (dim >= dm) qf[qc][c] = Frag{};
+    }
 
-  // DMA: element offset of the chunk this lane copies, per copy.
+  // DMA: byte offset of the chunk this lane copies, per copy. Chunks of
+  // dims from dm on take an offset past every range (the launcher keeps
+  // padded heads under 2^31 bytes), so they read zeros.
+  constexpr int kNoData = static_cast<int>(0x80000000u);
   int k_src[kCopies], v_src[kCopies];
 #pragma unroll
   for (int j = 0; j < kCopies; ++j) {
     const int slot = (wave * kCopies + j) * 64 + lane;
     const int row = slot / L::kChunks;
     const int phys = slot % L::kChunks;
-    k_src[j] = row * D + L::kElems * (phys ^ L::swizzle_k(row));
-    v_src[j] = row * D + L::kElems * (phys ^ L::swizzle_v(row));
+    const int kd = L::kElems * (phys ^ L::swizzle_k(row));
+    const int vd = L::kElems * (phys ^ L::swizzle_v(row));
+    k_src[j] = kd < dm ? (row * dm + kd) * L::kSize : kNoData;
+    v_src[j] = vd < dm ? (row * dm + vd) * L::kSize : kNoData;
   }
   // Buffer resources over the rest of this head's K and V from the tile's
-  // first key (the launcher guarantees S * D * sizeof(T) < 2^32): the per-lane byte
+  // first key (the launcher guarantees S * dm * sizeof(T) < 2^32): the per-lane byte
   // offsets stay in 32-bit VGPRs and the base is scalar, so a tile's copies
   // cost no vector address arithmetic. The hardware range-checks only the
   // per-lane offset against the resource's size (the scalar offset is
   // exempt), so the tile's position goes into the base, not the scalar
   // offset: keys from S on then fall outside the range and read zeros,
   // never the next head or memory past the tensor.
-  const unsigned head_bytes = static_cast<unsigned>(S) * D * L::kSize;
-#pragma unroll
-  for (int j = 0; j < kCopies; ++j) {
-    k_src[j] *= L::kSize;  // elements -> bytes
-    v_src[j] *= L::kSize;
-  }
+  const unsigned head_bytes = static_cast<unsigned>(S) * dm * L::kSize;
   // The copies' LDS destinations (M0) are wave-uniform: derived from a
   // scalar copy of the wave index, they stay in scalar registers instead of
   // costing a v_readfirstlane per copy and tile.
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto issue = [&](unsigned char* st, int key0) {
     // key0 < S for every issued tile, so 0 < rest <= head_bytes < 2^32
-    const unsigned tile_bytes = static_cast<unsigned>(key0) * D * L::kSize;
+    const unsigned tile_bytes = static_cast<unsigned>(key0) * dm * L::kSize;
     const unsigned rest = head_bytes - tile_bytes;
-    const std::size_t tile_elems = static_cast<std::size_t>(key0) * D;
+    const std::size_t tile_elems = static_cast<std::size_t>(key0) * dm;
 #pragma unroll
     for (int j = 0; j < kCopies; ++j)
       opl::buffer_copy16_lds(kh + tile_elems, rest, st + (wave_s * kCopies + j) * 1024,
@@ -1245,7 +1251,7 @@ void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     const int r0 = (v % kGroups) * kWaveRows;
     const int rr = lane / kChunks4;
     const int cc = lane % kChunks4;
-    float* const obase = O + head + static_cast<std::size_t>(q0 + kRowsPerWave * bw) * D;
+    float* const obase = O + head + static_cast<std::size_t>(q0 + kRowsPerWave * bw) * dm;
 #pragma unroll
     for (int i = 0; i < kWaveRows / kRowsPerStore; ++i) {
       const int row = r0 + kRowsPerStore * i + rr;
@@ -1260,8 +1266,8 @@ void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
         x.w += y.w;
       }
       const float4v xv = {x.x, x.y, x.z, x.w};
-      if (q0 + kRowsPerWave * bw + row < S)
-        __builtin_nontemporal_store(xv, reinterpret_cast<float4v*>(obase + static_cast<std::size_t>(row) * D) + cc);
+      if (q0 + kRowsPerWave * bw + row < S && 4 * cc < dm)
+        __builtin_nontemporal_store(xv, reinterpret_cast<float4v*>(obase + static_cast<std::size_t>(row) * dm) + cc);
     }
     return;
   }
@@ -1293,14 +1299,14 @@ void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     constexpr int kRowsPerStore = opl::kWaveSize / kChunks4;
     const int rr = lane / kChunks4;
     const int cc = lane % kChunks4;
-    float* const obase = O + head + static_cast<std::size_t>(wave_row0) * D;
+    float* const obase = O + head + static_cast<std::size_t>(wave_row0) * dm;
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / kRowsPerStore; ++i) {
       const int row = kRowsPerStore * i + rr;
       const float4 x = stg[row * kChunks4 + (cc ^ (row % kChunks4))];
       const float4v xv = {x.x, x.y, x.z, x.w};
-      if (wave_row0 + row < S)
-        __builtin_nontemporal_store(xv, reinterpret_cast<float4v*>(obase + static_cast<std::size_t>(row) * D) + cc);
+      if (wave_row0 + row < S && 4 * cc < dm)
+        __builtin_nontemporal_store(xv, reinterpret_cast<float4v*>(obase + static_cast<std::size_t>(row) * dm) + cc);
     }
   }
 }
@@ -1308,13 +1314,23 @@ void attention_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
 #undef OPL_LDS
 }  // namespace dma
 
-// True when the fast path applies (head_dim 64 or 128, aligned tensors).
+// True when the fast path applies: aligned tensors whose head dim is 64 or
+// 128, or any other whole number of 16-byte chunks up to 128, which runs
+// the instances of the next of 64 and 128 with the dims past it zero (its
+// K/V chunks take an out-of-range offset of 2^31 bytes, so such heads must
+// stay below that).
+inline int dma_layout(int head_dim) { return head_dim <= 64 ? 64 : 128; }
+
 inline bool dma_ok(const void* q, const void* k, const void* v, const void* out,
                    int sequence, int head_dim, unsigned element_bytes) {
   // one head of K or V must be addressable with 32-bit buffer offsets
   const unsigned long long head_bytes =
       static_cast<unsigned long long>(sequence) * head_dim * element_bytes;
-  return (head_dim == 64 || head_dim == 128) && head_bytes < (1ull << 32) &&
+  const bool native = head_dim == 64 || head_dim == 128;
+  const bool padded = !native && head_dim <= 128 &&
+                      head_dim % static_cast<int>(16 / element_bytes) == 0 &&
+                      head_bytes < (1ull << 31);
+  return (native ? head_bytes < (1ull << 32) : padded) &&
          opl::aligned16(q) && opl::aligned16(k) && opl::aligned16(v) &&
          opl::aligned16(out);
 }
@@ -1345,8 +1361,9 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
     // Grids too small to fill the CUs split each query block's keys
     // between groups of wavefronts in the workgroup; the smallest also
     // halve the query block (and, fp16 at D = 128, split its keys four ways).
+    const int layout = dma_layout(head_dim);
     const long long half_up_to =
-        head_dim == 128 ? dma::kHalfRowsUpTo
+        layout == 128 ? dma::kHalfRowsUpTo
                         : (causal ? dma::kHalfRowsUpToD64Causal : dma::kHalfRowsUpToD64);
     const bool half_rows = blocks <= half_up_to;
     const bool split = half_rows ||
@@ -1356,51 +1373,51 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
     const long long padded = (wgs + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
     const dim3 grid(static_cast<unsigned>(padded));
     if constexpr (sizeof(T) == 2) {
-      if (head_dim == 128) {
+      if (layout == 128) {
         // 64-row blocks x 4 groups / 128-row blocks x 2 groups: 8 wavefronts
         const dim3 block(split ? 2 * kThreads : kThreads);
         if (half_rows)
           dma::attention_dma_kernel<T, 128, 4, 2, 32><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
         else if (split)
           dma::attention_dma_kernel<T, 128, 2, 4, 64><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
         else
           dma::attention_dma_kernel<T, 128, 1, 4, 64><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
       } else {
         // (split implies half_rows at D = 64; 4 wavefronts either way)
         const dim3 block(kThreads);
         if (half_rows)
           dma::attention_dma_kernel<T, 64, 2, 2, 64><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
         else
           dma::attention_dma_kernel<T, 64, 1, 4, 64><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
       }
     } else {
       // fp32: 32-key tiles, at most two groups (a group's K/V stages hold
       // 64 KiB at D = 128): 64-row blocks with two groups of 2 wavefronts,
       // 128-row blocks with two groups of 4, or one group of 4.
-      if (head_dim == 128) {
+      if (layout == 128) {
         const dim3 block(split && !half_rows ? 2 * kThreads : kThreads);
         if (half_rows)
           dma::attention_dma_kernel<T, 128, 2, 2, 32><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
         else if (split)
           dma::attention_dma_kernel<T, 128, 2, 4, 32><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
         else
           dma::attention_dma_kernel<T, 128, 1, 4, 32><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
       } else {
         const dim3 block(kThreads);
         if (half_rows)
           dma::attention_dma_kernel<T, 64, 2, 2, 32><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
         else
           dma::attention_dma_kernel<T, 64, 1, 4, 32><<<grid, block, 0, stream>>>(
-              q, k, v, out, bh, sequence, c, scale);
+              q, k, v, out, bh, sequence, head_dim, c, scale);
       }
     }
     return hipGetLastError();

@@ -1008,7 +1008,52 @@ def test_attention_f32_fast_path(hip, heads, s, d, causal):
 POISON_CASES = [(1, 300, 128, False), (2, 1000, 128, True), (50, 300, 128, False),
                 (20, 1000, 128, True), (100, 300, 128, False), (70, 1000, 128, True),
                 (1, 1000, 64, True), (3, 300, 64, False), (200, 300, 64, True),
-                (60, 1000, 64, False)]
+                (60, 1000, 64, False),
+                # head dims padded to the 64 / 128 layouts (dims past D read zeros)
+                (1, 300, 96, False), (20, 1000, 80, True), (100, 300, 96, False),
+                (3, 300, 48, True), (200, 300, 32, False)]
+
+
+# Head dims other than 64 and 128 (whole 16-byte chunks) run the 64 / 128
+# fast-path instances with the dims past D zero in Q, K and V; only D
+# columns of O are stored. (heads, S, D, causal) over 64-row blocks, split
+# keys and unsplit grids.
+PADDED_CASES = [(2, 333, 96, False), (12, 1000, 80, True), (100, 300, 96, True),
+                (300, 129, 120, False), (4, 200, 8, False), (50, 300, 16, True),
+                (200, 300, 40, False), (520, 100, 56, True)]
+
+
+@pytest.mark.parametrize("heads,s,d,causal", PADDED_CASES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_attention_padded_head_dims(lib, heads, s, d, causal, dtype):
+    q, k, v = _attn_inputs(s, d, False, 1300 + heads + d, heads=heads)
+    n = heads * s * d
+    guard = 64 * d
+    out_flat = torch.full((n + guard,), float("nan"), dtype=torch.float32, device="cuda")
+    if dtype == "f16":
+        bits = [oracle.to_f16_bits(t) for t in (q, k, v)]
+        dq, dk, dv = (to_device(b) for b in bits)
+        ref_in = [oracle.from_f16_bits(b) for b in bits]
+        fn, tol = lib.operatorlib_attention_f16, None
+    else:
+        dq, dk, dv = (to_device(t) for t in (q, k, v))
+        ref_in = [q, k, v]
+        fn, tol = lib.operatorlib_attention_f32, 1e-4
+    check(fn(ptr(dq), ptr(dk), ptr(dv), ptr(out_flat), 1, heads, s, d, int(causal),
+             stream_handle()), "attention")
+    torch.cuda.synchronize()
+    flat = out_flat.cpu().numpy().astype(np.float64)
+    assert np.isnan(flat[n:]).all()  # nothing stored past the output
+    y = flat[:n].reshape(heads, s, d)
+    rng = np.random.default_rng(1301)
+    hs = np.concatenate([np.full(s, heads - 1), rng.integers(0, heads, 256)]).astype(np.int32)
+    rs = np.concatenate([np.arange(s), rng.integers(0, s, 256)]).astype(np.int32)
+    ref = oracle.attention(*ref_in, causal, hs, rs)
+    assert np.isfinite(y).all()
+    if tol is None:
+        assert np.max(np.abs(y[hs, rs] - ref)) <= 2e-3
+    else:
+        assert np.all(np.abs(y[hs, rs] - ref) <= tol + tol * np.abs(ref))
 
 
 @pytest.mark.parametrize("heads,s,d,causal", POISON_CASES)

@@ -142,9 +142,11 @@ def test_gemm_ws_matches_plain(lib, m, n, k, dtype):
         assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-4
 
 
-@pytest.mark.parametrize("dtype,heads,s,d,causal", [("f32", 4, 256, 96, False),
+# head dims that are not whole 16-byte chunks take the register-staged
+# kernel, whose small grids split keys through scratch
+@pytest.mark.parametrize("dtype,heads,s,d,causal", [("f32", 4, 256, 99, False),
                                                     ("f32", 2, 300, 71, True),
-                                                    ("f16", 3, 256, 96, False)])
+                                                    ("f16", 3, 256, 100, False)])
 def test_attention_ws_matches_plain(lib, dtype, heads, s, d, causal):
     q, k, v = (oracle.normal(73 + i, (1, heads, s, d)) for i in range(3))
     if dtype == "f16":

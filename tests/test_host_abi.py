@@ -283,11 +283,15 @@ def test_ws_rejects_misaligned_workspace(lib):
 
 def test_attention_workspace_size(lib):
     q = lib.operatorlib_attention_f32_workspace_size
-    # B1 H4 S256 D96 (register-staged): 8 query blocks of 128 rows; 4 key
-    # splits (256 / 8 workgroups capped at 4) of [rows][D + 2]
-    assert q(FAKE, FAKE, FAKE, FAKE, 1, 4, 256, 96, 0) == 4 * 4 * 256 * 98 * 4
-    # D 128 on aligned tensors: the direct-to-LDS kernel, no scratch
+    # B1 H4 S256 D99 (not whole 16-byte chunks: register-staged): 8 query
+    # blocks of 128 rows; 4 key splits (256 / 8 workgroups capped at 4) of
+    # [rows][D + 2]
+    assert q(FAKE, FAKE, FAKE, FAKE, 1, 4, 256, 99, 0) == 4 * 4 * 256 * 101 * 4
+    # D 128, and any whole number of chunks (D 96: the D 128 instances with
+    # zero dims past 96), on aligned tensors: the direct-to-LDS kernel, no
+    # scratch
     assert q(FAKE, FAKE, FAKE, FAKE, 1, 4, 256, 128, 0) == 0
+    assert q(FAKE, FAKE, FAKE, FAKE, 1, 4, 256, 96, 0) == 0
     assert q(FAKE, FAKE, FAKE, FAKE, 1, 4, 256, 129, 0) == 0  # invalid: D > 128
     h = lib.operatorlib_attention_f16_workspace_size
     assert h(FAKE, FAKE, FAKE, FAKE, 4, 32, 8192, 128, 1) == 0  # fast path: none

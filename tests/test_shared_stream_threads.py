@@ -8,7 +8,7 @@ library together):
   * gemm_f16 1 x 1024 x 4096 (decode GEMM, split-K partials + split sum);
   * gemm_f16 1000^3 (64 tiles of 128 x 128, fewer than the CUs: every
     tile split along K into partial tiles, then the split sum);
-  * attention_f32 B1 H4 S256 D96 (register-staged on a small grid: keys
+  * attention_f32 B1 H4 S256 D99 (register-staged on a small grid: keys
     split over workgroups, partials, then the combine kernel);
   * gemm_f16 4352 x 4096 x 512 (272 tiles of 256 x 256: the last round's 16
     tiles are split along K, partial tiles, then the tail sum).
@@ -53,10 +53,11 @@ HIP_STREAM_PER_THREAD = 2  # hipStreamPerThread, include/hip/hip_runtime_api.h
 # every 256-row tile row, its first and last.
 TAIL_MK = (4352, 512)
 TAIL_N = 4096
-# attention head dim: 96 takes the register-staged kernel, whose small
-# grids split keys over workgroups through scratch (64 and 128 on aligned
-# tensors take the direct-to-LDS kernel, which needs none)
-ATTN_D = 96
+# attention head dim: 99 (not a whole number of 16-byte chunks) takes the
+# register-staged kernel, whose small grids split keys over workgroups
+# through scratch (chunk-multiple dims on aligned tensors take the
+# direct-to-LDS kernel, which needs none)
+ATTN_D = 99
 TAIL_ROWS = np.array(sorted({r for t in range(0, TAIL_MK[0], 256) for r in (t, t + 255)}),
                      dtype=np.int32)
 
