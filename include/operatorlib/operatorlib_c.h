@@ -52,7 +52,7 @@ extern "C" {
 typedef uint16_t operatorlib_half_t;
 
 /* Version of this ABI; bumped on any incompatible change. */
-#define OPERATORLIB_ABI_VERSION 2
+#define OPERATORLIB_ABI_VERSION 3
 int operatorlib_abi_version(void);
 
 /* Human-readable text for a status returned by any entry point. */

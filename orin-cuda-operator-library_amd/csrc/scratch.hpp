@@ -7,6 +7,9 @@
 // Users (each sizes its plan to the scratch it is offered; less scratch
 // means fewer splits or a slower kernel, never an error):
 //   * reduce: one fp64 partial per workgroup (at most 2 KiB);
+//   * softmax and RMSNorm rows split over workgroups (rows longer than
+//     32768 columns, or few rows longer than 4096): one partial per row
+//     and segment (8 or 4 bytes);
 //   * decode GEMMs (M <= 16): split-K partial sums;
 //   * large fp16 GEMMs whose rows are not 4-byte aligned: operand copies
 //     with chunk-padded rows;

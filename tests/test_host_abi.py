@@ -80,7 +80,7 @@ def test_exported_dynamic_symbols_are_exactly_the_abi():
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.operatorlib_abi_version() == 2
+    assert lib.operatorlib_abi_version() == 3
     assert lib.operatorlib_status_string(0)
     assert b"invalid" in lib.operatorlib_status_string(INVALID).lower()
 
