@@ -653,6 +653,14 @@ constexpr long long kHalfRowsUpToD64Causal = 512;
 static_assert(kHalfRowsUpToD64 >= kSplitKeysBelow - 1 &&
                   kHalfRowsUpToD64Causal >= kSplitKeysBelowCausal - 1,
               "every D = 64 grid that splits keys runs 64-row blocks");
+// Sequences of at most this many tokens on grids past kHalfRowsUpTo blocks
+// run 64-row blocks of two wavefronts on 32-key tiles (16 or 32 KiB of LDS
+// instead of 64): a 128-row block held 128 rows for S of them, and its LDS
+// let two workgroups share a CU, so launches of many short heads ran in
+// latency-bound rounds. Measured on MI355X, fp16 (us, before -> after;
+// SDPA): B128 H32 S16 D128 45.3 -> 21.5 (15.2); B16 H32 S1 7.9 -> 6.0
+// (12.7); S = 128 was no faster (B32 H32 S128 30.9 vs 32.6).
+constexpr int kShortSequence = 64;
 // Headroom (log2 units) the running row max may lag the true max by.
 constexpr float kLazyLog2 = 8.0f;
 
@@ -1373,6 +1381,18 @@ int attention_entry(const T* q, const T* k, const T* v, float* out, int batch,
     const long long padded = (wgs + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
     const dim3 grid(static_cast<unsigned>(padded));
     if constexpr (sizeof(T) == 2) {
+      if (sequence <= dma::kShortSequence && !half_rows) {
+        const long long tb = (sequence + 63) / 64 * static_cast<long long>(bh);
+        const long long tw = (tb + dma::kXcds - 1) / dma::kXcds * dma::kXcds;
+        const dim3 tgrid(static_cast<unsigned>(tw));
+        if (layout == 128)
+          dma::attention_dma_kernel<T, 128, 1, 2, 32><<<tgrid, dim3(kThreads / 2), 0, stream>>>(
+              q, k, v, out, bh, sequence, head_dim, c, scale);
+        else
+          dma::attention_dma_kernel<T, 64, 1, 2, 32><<<tgrid, dim3(kThreads / 2), 0, stream>>>(
+              q, k, v, out, bh, sequence, head_dim, c, scale);
+        return hipGetLastError();
+      }
       if (layout == 128) {
         // 64-row blocks x 4 groups / 128-row blocks x 2 groups: 8 wavefronts
         const dim3 block(split ? 2 * kThreads : kThreads);

@@ -1023,6 +1023,20 @@ PADDED_CASES = [(2, 333, 96, False), (12, 1000, 80, True), (100, 300, 96, True),
                 (200, 300, 40, False), (520, 100, 56, True)]
 
 
+# Short sequences (S <= 64) on more than 128 heads: 64-row blocks of two
+# wavefronts on 32-key tiles, both layouts, padded dims included.
+@pytest.mark.parametrize("heads,s,d,causal", [(200, 16, 128, False), (300, 64, 64, True),
+                                              (150, 1, 128, False), (140, 33, 96, True),
+                                              (260, 7, 40, False), (129, 64, 128, True)])
+def test_attention_f16_short_sequences(hip, heads, s, d, causal):
+    q, k, v = _attn_inputs(s, d, False, 1400 + heads + s, heads=heads)
+    qb, kb, vb = (oracle.to_f16_bits(t) for t in (q, k, v))
+    ref = oracle.attention(*(oracle.from_f16_bits(t) for t in (qb, kb, vb)), causal)
+    y = hip.attention(qb, kb, vb, causal)
+    assert np.isfinite(y).all()
+    assert np.max(np.abs(y - ref)) <= 2e-3
+
+
 @pytest.mark.parametrize("heads,s,d,causal", PADDED_CASES)
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_attention_padded_head_dims(lib, heads, s, d, causal, dtype):
