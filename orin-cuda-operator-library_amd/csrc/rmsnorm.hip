@@ -260,9 +260,9 @@ __global__ __launch_bounds__(kSplitThreads) void rmsnorm_split_stats_kernel(
   using Chunk = typename opl::RowElem<T>::Chunk;
   constexpr int E = opl::RowElem<T>::kPerChunk;
   __shared__ float slots[kSplitWaves];
-  const int c0 = blockIdx.x * seg_len;
+  const int c0 = blockIdx.y * seg_len;
   const int n = min(cols - c0, seg_len);
-  const T* p = input + static_cast<std::size_t>(blockIdx.y) * cols + c0;
+  const T* p = input + static_cast<std::size_t>(blockIdx.x) * cols + c0;
   const opl::Segment<T> sg(p, n);
   const Chunk* body = reinterpret_cast<const Chunk*>(p + sg.head);
   const int t = threadIdx.x;
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(kSplitThreads) void rmsnorm_split_stats_kernel(
     ss += x * x;
   }
   ss = opl::block_reduce<opl::SumOp, kSplitWaves>(ss, slots);
-  if (t == 0) partials[static_cast<std::size_t>(blockIdx.y) * gridDim.x + blockIdx.x] = ss;
+  if (t == 0) partials[static_cast<std::size_t>(blockIdx.x) * gridDim.y + blockIdx.y] = ss;
 }
 
 // kChunks: input and output rows share their 16-byte phase (16-byte
@@ -303,16 +303,16 @@ __global__ __launch_bounds__(kSplitThreads) void rmsnorm_split_apply_kernel(
     const float* __restrict__ partials, int cols, int seg_len, float epsilon) {
   using Chunk = typename opl::RowElem<T>::Chunk;
   constexpr int E = opl::RowElem<T>::kPerChunk;
-  const int segments = gridDim.x;
-  const float* pr = partials + static_cast<std::size_t>(blockIdx.y) * segments;
+  const int segments = gridDim.y;
+  const float* pr = partials + static_cast<std::size_t>(blockIdx.x) * segments;
   const int lane = threadIdx.x % opl::kWaveSize;
   float ps = 0.0f;
   for (int i = lane; i < segments; i += opl::kWaveSize) ps += pr[i];
   const float inv = rsqrtf(opl::wave_reduce<opl::SumOp>(ps) / static_cast<float>(cols) + epsilon);
 
-  const int c0 = blockIdx.x * seg_len;
+  const int c0 = blockIdx.y * seg_len;
   const int n = min(cols - c0, seg_len);
-  const std::size_t offset = static_cast<std::size_t>(blockIdx.y) * cols + c0;
+  const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols + c0;
   const T* p = input + offset;
   const T* w = weight + c0;
   T* o = output + offset;
@@ -442,7 +442,8 @@ int rmsnorm_launch(const Args<T>& args, const opl::ScratchSource& src, hipStream
     opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
     if (lease.status() != hipSuccess) return lease.status();
     float* partials = static_cast<float*>(lease.data());
-    const dim3 grid(static_cast<unsigned>(split.segments), static_cast<unsigned>(args.rows));
+    // rows on x (up to 2^31 - 1), segments (at most 512) on y
+    const dim3 grid(static_cast<unsigned>(args.rows), static_cast<unsigned>(split.segments));
     rmsnorm_split_stats_kernel<T><<<grid, dim3(kSplitThreads), 0, stream>>>(
         args.input, partials, hidden, split.seg_len);
     const hipError_t status = hipGetLastError();

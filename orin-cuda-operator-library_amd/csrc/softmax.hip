@@ -289,9 +289,9 @@ __global__ __launch_bounds__(kSplitThreads) void softmax_split_stats_kernel(
   constexpr int E = opl::RowElem<T>::kPerChunk;
   __shared__ float max_slots[kSplitWaves];
   __shared__ float sum_slots[kSplitWaves];
-  const int c0 = blockIdx.x * seg_len;
+  const int c0 = blockIdx.y * seg_len;
   const int n = min(cols - c0, seg_len);
-  const T* p = input + static_cast<std::size_t>(blockIdx.y) * cols + c0;
+  const T* p = input + static_cast<std::size_t>(blockIdx.x) * cols + c0;
   const opl::Segment<T> sg(p, n);
   const Chunk* body = reinterpret_cast<const Chunk*>(p + sg.head);
   const int t = threadIdx.x;
@@ -324,7 +324,7 @@ __global__ __launch_bounds__(kSplitThreads) void softmax_split_stats_kernel(
   const float seg_sum = opl::block_reduce<opl::SumOp, kSplitWaves>(
       s * opl::fast_exp2((m - seg_max) * kLog2e), sum_slots);
   if (t == 0)
-    partials[static_cast<std::size_t>(blockIdx.y) * gridDim.x + blockIdx.x] =
+    partials[static_cast<std::size_t>(blockIdx.x) * gridDim.y + blockIdx.y] =
         make_float2(seg_max, seg_sum);
 }
 
@@ -336,8 +336,8 @@ __global__ __launch_bounds__(kSplitThreads) void softmax_split_apply_kernel(
     const float2* __restrict__ partials, int cols, int seg_len) {
   using Chunk = typename opl::RowElem<T>::Chunk;
   constexpr int E = opl::RowElem<T>::kPerChunk;
-  const int segments = gridDim.x;
-  const float2* pr = partials + static_cast<std::size_t>(blockIdx.y) * segments;
+  const int segments = gridDim.y;
+  const float2* pr = partials + static_cast<std::size_t>(blockIdx.x) * segments;
   const int lane = threadIdx.x % opl::kWaveSize;
   float pm = -FLT_MAX;
   for (int i = lane; i < segments; i += opl::kWaveSize) pm = fmaxf(pm, pr[i].x);
@@ -348,9 +348,9 @@ __global__ __launch_bounds__(kSplitThreads) void softmax_split_apply_kernel(
   const float inv = 1.0f / opl::wave_reduce<opl::SumOp>(ps);
   auto f = [&](float x) { return opl::fast_exp2((x - row_max) * kLog2e) * inv; };
 
-  const int c0 = blockIdx.x * seg_len;
+  const int c0 = blockIdx.y * seg_len;
   const int n = min(cols - c0, seg_len);
-  const std::size_t offset = static_cast<std::size_t>(blockIdx.y) * cols + c0;
+  const std::size_t offset = static_cast<std::size_t>(blockIdx.x) * cols + c0;
   const T* p = input + offset;
   T* o = output + offset;
   const int t = threadIdx.x;
@@ -444,7 +444,8 @@ int softmax_launch(const T* input, T* output, int rows, int cols,
     opl::ScratchLease lease(stream, src.workspace_mode ? src.data : nullptr, src.bytes);
     if (lease.status() != hipSuccess) return lease.status();
     float2* partials = static_cast<float2*>(lease.data());
-    const dim3 grid(static_cast<unsigned>(split.segments), static_cast<unsigned>(rows));
+    // rows on x (up to 2^31 - 1), segments (at most 512) on y
+    const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>(split.segments));
     softmax_split_stats_kernel<T><<<grid, dim3(kSplitThreads), 0, stream>>>(
         input, partials, cols, split.seg_len);
     const hipError_t status = hipGetLastError();

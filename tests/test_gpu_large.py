@@ -70,6 +70,32 @@ def test_rows_past_2g_elements(lib, op):
     assert rel.max() <= 1e-5
 
 
+@pytest.mark.parametrize("op", ["softmax", "rmsnorm"])
+def test_long_rows_past_the_grid_y_limit(lib, op):
+    # Rows past 32768 columns are split over workgroups, one grid row per
+    # matrix row: more than 65535 of them (the limit of a grid's y and z
+    # dimensions) must still launch, and every row be written.
+    rows, cols = 65540, 32769
+    assert rows * cols > BIG
+    x = _randn((rows, cols), 15, scale=3.0 if op == "softmax" else 1.0)
+    y = torch.full_like(x, float("nan"))
+    if op == "softmax":
+        check(lib.operatorlib_softmax_f32(ptr(x), ptr(y), rows, cols, stream_handle()), op)
+    else:
+        w = torch.rand(cols, device="cuda") + 0.5
+        check(lib.operatorlib_rmsnorm_f32(ptr(x), ptr(w), ptr(y), rows, cols, 1e-6,
+                                          stream_handle()), op)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y[-1]).any() and not torch.isnan(y[:, -1]).any()
+    r = torch.from_numpy(_rows(rows, 16, 10)).cuda()
+    xs = x[r].cpu().numpy()
+    ys = y[r].cpu().numpy().astype(np.float64)
+    ref = oracle.softmax(xs) if op == "softmax" else oracle.rmsnorm(xs, w.cpu().numpy(), 1e-6)
+    rel = np.abs(ys - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert rel.max() <= 1e-5
+    del x, y
+
+
 def test_transpose_past_2g_elements(lib):
     n = 46349  # n * n > 2^31; not a multiple of 4: the 4-byte tile kernel
     assert n * n > BIG
