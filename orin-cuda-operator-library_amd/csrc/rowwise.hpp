@@ -317,7 +317,8 @@ inline SplitPlan split_plan(int rows, int cols) {
   if (cols <= kRowWaveMaxCols) return p;
   const bool long_rows = cols > kRowBlockMaxCols;
   if (!long_rows && rows >= kSplitMaxRows) return p;
-  const int by_rows = (kSplitTargetBlocks + rows - 1) / rows;
+  const int by_rows =
+      static_cast<int>((static_cast<long long>(kSplitTargetBlocks) + rows - 1) / rows);
   const int by_cols = cols / kSplitMinSegment;
   const int want = by_rows < by_cols ? by_rows : by_cols;
   if (want < (long_rows ? 1 : 2)) return p;

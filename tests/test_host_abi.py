@@ -249,6 +249,7 @@ def test_rowwise_workspace_size(lib):
         assert q(4, 1 << 20) == pair * 4 * 128       # 128 segments of 8192
         assert q(600, 40000) == pair * 600           # one segment per row
         assert q(0, 5000) == 0 and q(3, 0) == 0      # invalid sizes
+        assert q(2**31 - 1, 40000) == pair * (2**31 - 1)  # one segment per row
 
 
 def test_rowwise_ws_reject_short_workspace(lib):
