@@ -14,10 +14,13 @@
 // 16-byte chunks). The whole row is read from HBM exactly once and written
 // exactly once.
 //
-// Launch shapes (chosen by pick_row_plan):
+// Launch shapes:
+//   short rows     groups of G <= 32 lanes per row (up to 32 elements, or
+//                  32 chunks of aligned rows; group_reduce)
 //   cols <= 4096   one wavefront per row, 4 rows per 256-thread workgroup
-//   cols <= 32768  one 512-thread workgroup per row
-//   larger         two passes over HBM (row does not fit in registers)
+//   cols <= 32768  one 512-thread workgroup per row (pick_row_plan)
+//   longer rows,   segments over workgroups, two passes over HBM
+//   few long rows  (split_plan, Segment)
 
 #include <hip/hip_runtime.h>
 
