@@ -3,7 +3,9 @@
 // Reference: operatorlib::transpose_f32 (src/transpose.cu:38-47) with a
 // 32x33 padded shared tile and 32x8 thread blocks sized for 32-lane warps.
 //
-// MI355X design, four kernels:
+// MI355X design, four tiled kernels, and two for thin matrices (at most 8
+// rows or columns: transpose_thin4_kernel / transpose_thin_kernel, one
+// thread per 4 or 1 indices of the long side; described before them):
 //   * transpose_vec4_kernel (rows and cols multiples of 4, 16-byte aligned
 //     buffers): a 128x128 fp32 tile per 512-thread workgroup, moved with
 //     16-byte loads and stores in both directions. The 64 KiB tile sits in
@@ -126,6 +128,73 @@ __global__ __launch_bounds__(kThinThreads) void transpose_thin_kernel(
       }
     }
   }
+}
+
+// The same for a long side that is a multiple of 4 with 16-byte aligned
+// buffers: a thread moves 4 consecutive indices of the long side as S
+// float4 loads and S float4 stores (the S x 4 block transposed in
+// registers; S is exact, so every register index is a constant), instead
+// of 4 S scalar accesses. The long side's accesses are contiguous per
+// wavefront and non-temporal; the short side's (16 bytes every 16 S) are
+// cached, so that L2 merges the partial lines.
+typedef float float4t __attribute__((ext_vector_type(4)));
+
+template <int S, bool kShortRows>
+__global__ __launch_bounds__(kThinThreads) void transpose_thin4_kernel(
+    const float* __restrict__ input, float* __restrict__ output, long long n) {
+  const long long groups = n / 4;
+  for (long long g = static_cast<long long>(blockIdx.x) * kThinThreads + threadIdx.x;
+       g < groups; g += static_cast<long long>(gridDim.x) * kThinThreads) {
+    const long long i0 = 4 * g;
+    float v[4 * S];
+    if constexpr (kShortRows) {
+      // v[4 j + a] = input[j][i0 + a]; output row i0 + a holds v[4 j + a]
+      // at column j, so its flat element e = a S + j
+#pragma unroll
+      for (int j = 0; j < S; ++j) {
+        const float4t q = __builtin_nontemporal_load(
+            reinterpret_cast<const float4t*>(input + j * n + i0));
+#pragma unroll
+        for (int a = 0; a < 4; ++a) v[4 * j + a] = q[a];
+      }
+#pragma unroll
+      for (int f = 0; f < S; ++f) {
+        float4t o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = v[4 * ((4 * f + c) % S) + (4 * f + c) / S];
+        // cached: a store instruction writes 16 of every 16 S bytes, and the
+        // wavefront's S stores complete the lines in L2 (non-temporal partial
+        // lines: 8 x 2^20 67 us against 25 for the scalar kernel)
+        *reinterpret_cast<float4t*>(output + i0 * S + 4 * f) = o;
+      }
+    } else {
+      // rows i0 .. i0 + 3 of S columns are 4 S consecutive floats: v[a S + j]
+#pragma unroll
+      for (int f = 0; f < S; ++f) {
+        const float4t q = *reinterpret_cast<const float4t*>(input + i0 * S + 4 * f);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[4 * f + c] = q[c];
+      }
+#pragma unroll
+      for (int j = 0; j < S; ++j) {
+        float4t o;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) o[a] = v[a * S + j];
+        __builtin_nontemporal_store(o, reinterpret_cast<float4t*>(output + j * n + i0));
+      }
+    }
+  }
+}
+
+template <bool kShortRows, int S = 1>
+void launch_thin4(const float* input, float* output, int s, long long n, hipStream_t stream) {
+  if constexpr (S < kThinMax) {
+    if (s > S) return launch_thin4<kShortRows, S + 1>(input, output, s, n, stream);
+  }
+  const long long blocks = (n / 4 + kThinThreads - 1) / kThinThreads;
+  transpose_thin4_kernel<S, kShortRows>
+      <<<dim3(static_cast<unsigned>(blocks < kThinMaxBlocks ? blocks : kThinMaxBlocks)),
+         dim3(kThinThreads), 0, stream>>>(input, output, n);
 }
 
 template <bool kShortRows, int S = 1>
@@ -506,6 +575,15 @@ extern "C" int operatorlib_transpose_f32(const float* input, float* output,
   hipStream_t stream = static_cast<hipStream_t>(stream_handle);
   constexpr long long kMaxGrid = 1LL << 30;
   if (rows <= kThinMax || cols <= kThinMax) {
+    const int s = rows <= cols ? rows : cols;  // <= kThinMax
+    const long long n = rows <= cols ? cols : rows;
+    if (n % 4 == 0 && opl::aligned16(input) && opl::aligned16(output)) {
+      if (rows <= cols)
+        launch_thin4<true>(input, output, s, n, stream);
+      else
+        launch_thin4<false>(input, output, s, n, stream);
+      return hipGetLastError();
+    }
     if (rows <= cols)
       launch_thin<true>(input, output, rows, cols, stream);
     else

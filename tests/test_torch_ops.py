@@ -45,8 +45,11 @@ def test_reduce_sum_on_side_stream(ops, side_stream):
     assert abs(out.item() - ref) <= 1e-5 * max(abs(ref), np.abs(x).sum() * 1e-7)
 
 
+# (3, 50001) and (2, 40000) are split over workgroups: the binding passes a
+# workspace from torch's allocator to the *_ws entry point
 @pytest.mark.parametrize("rows,cols,scale", [(19, 128, 5.0), (17, 1024, 5.0),
-                                             (17, 1003, 1000.0)])
+                                             (17, 1003, 1000.0), (3, 50001, 5.0),
+                                             (100000, 8, 5.0)])
 def test_softmax_on_side_stream(ops, side_stream, rows, cols, scale):
     x = oracle.normal(102 + rows, (rows, cols), 0.0, scale)
     out = _run(side_stream, lambda: ops.softmax(_dev(x)))
@@ -71,7 +74,7 @@ def test_transpose_on_side_stream(ops, side_stream, rows, cols):
     assert np.array_equal(out.cpu().numpy(), x.T)
 
 
-@pytest.mark.parametrize("shape", [(3, 7, 1024), (5, 1003)])
+@pytest.mark.parametrize("shape", [(3, 7, 1024), (5, 1003), (2, 40000), (4, 65536)])
 def test_rmsnorm_on_side_stream(ops, side_stream, shape):
     x = oracle.normal(105, shape)
     w = oracle.normal(106, shape[-1])
