@@ -664,6 +664,58 @@ def extra_ops(torch, lib, oracle, ptr, names, steps, warmup):
         out.append(fl_entry("attention_f32", list(shape), eff, t, FP32_PEAK_TFLOPS,
                             {"causal": causal}))
         del qkv, o
+
+    # Shapes away from the BASELINE configs (no reference figure), one per
+    # path that a timing sweep against same-size copies and vendor kernels
+    # showed slow and that now has a kernel of its own: vocabulary-width
+    # softmax (rows split over workgroups), MoE-router softmax (lane groups),
+    # a long-row RMSNorm, a vector transpose, fp16 attention at head dim 96
+    # and on short sequences.
+    if want("shapes"):
+        tag = " (off-benchmark)"
+        for shape in ((32, 50257), (1048576, 8)):
+            x = torch.from_numpy(oracle.normal(26, shape, 0.0, 3.0))
+            nb = 8 * shape[0] * shape[1]
+            sets = sets_for(nb // 2)
+            xs = [(x.cuda(), torch.empty(shape, device=dev)) for _ in range(sets)]
+            f = lambda i: lib.operatorlib_softmax_f32(ptr(xs[i % sets][0]), ptr(xs[i % sets][1]),
+                                                      shape[0], shape[1], stream)
+            out.append(bw_entry("softmax_f32" + tag, list(shape), nb,
+                                time_launches(torch, f, steps, warmup)))
+            del xs
+        shape = (4, 1048576)
+        x = torch.from_numpy(oracle.normal(27, shape))
+        w = torch.from_numpy(oracle.uniform(28, shape[1], 0.5, 1.5)).cuda()
+        nb = (2 * shape[0] * shape[1] + shape[1]) * 4
+        sets = sets_for((shape[0] * shape[1] + shape[1]) * 4)
+        xs = [(x.cuda(), torch.empty(shape, device=dev)) for _ in range(sets)]
+        f = lambda i: lib.operatorlib_rmsnorm_f32(ptr(xs[i % sets][0]), ptr(w), ptr(xs[i % sets][1]),
+                                                  shape[0], shape[1], 1e-6, stream)
+        out.append(bw_entry("rmsnorm_f32" + tag, list(shape), nb,
+                            time_launches(torch, f, steps, warmup)))
+        del xs, w
+        shape = (1, 1048576)
+        x = torch.from_numpy(oracle.uniform(29, shape))
+        nb = 8 * shape[0] * shape[1]
+        sets = sets_for(nb // 2)
+        xs = [(x.cuda(), torch.empty(shape[::-1], device=dev)) for _ in range(sets)]
+        f = lambda i: lib.operatorlib_transpose_f32(ptr(xs[i % sets][0]), ptr(xs[i % sets][1]),
+                                                    shape[0], shape[1], stream)
+        out.append(bw_entry("transpose_f32" + tag, list(shape), nb,
+                            time_launches(torch, f, steps, warmup)))
+        del xs
+        for bsz, heads, seq, d in ((2, 32, 4096, 96), (128, 32, 16, 128)):
+            shape = (bsz, heads, seq, d)
+            gen = torch.Generator(device=dev).manual_seed(32)
+            qkv = [torch.randn(shape, device=dev, generator=gen).half() for _ in range(3)]
+            o = torch.empty(shape, device=dev)
+            f = lambda i: lib.operatorlib_attention_f16(ptr(qkv[0]), ptr(qkv[1]), ptr(qkv[2]),
+                                                        ptr(o), bsz, heads, seq, d, 0, stream)
+            t = time_launches(torch, f, max(5, min(steps, 20)), 3)
+            out.append(fl_entry("attention_f16" + tag, list(shape),
+                                4 * bsz * heads * seq * seq * d, t, FP16_PEAK_TFLOPS,
+                                {"causal": False}))
+            del qkv, o
     torch.cuda.empty_cache()
     return out
 
