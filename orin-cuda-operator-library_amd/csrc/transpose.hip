@@ -3,7 +3,7 @@
 // Reference: operatorlib::transpose_f32 (src/transpose.cu:38-47) with a
 // 32x33 padded shared tile and 32x8 thread blocks sized for 32-lane warps.
 //
-// MI355X design, four tiled kernels, and two for thin matrices (at most 8
+// MI355X design, four tiled kernels, and two for thin matrices (at most 16
 // rows or columns: transpose_thin4_kernel / transpose_thin_kernel, one
 // thread per 4 or 1 indices of the long side; described before them):
 //   * transpose_vec4_kernel (rows and cols multiples of 4, 16-byte aligned
@@ -99,9 +99,10 @@ __global__ __launch_bounds__(kThreads) void transpose_tile_kernel(
 // is looped over; its accesses are s floats apart, and the wavefront's s
 // accesses together cover one contiguous range. The tiled kernels spent
 // nearly whole tiles of padding here (1 x 2^20: 97.5 us, 2^20 x 3: 52 us,
-// against a 3.7 us copy of the same bytes). Loads are issued from clamped
-// indices, unconditionally, so they leave back to back.
-constexpr int kThinMax = 8;
+// against a 3.7 us copy of the same bytes; 2^20 x 16: 51.6 us, 13 x 100003:
+// 13.6 us, now 26.0 and 8.0). Loads are issued from clamped indices,
+// unconditionally, so they leave back to back.
+constexpr int kThinMax = 16;
 constexpr int kThinThreads = 256;
 constexpr int kThinMaxBlocks = 8192;
 

@@ -254,15 +254,19 @@ TRANSPOSE_SHAPES = [(37, 65), (64, 96), (65, 37), (1, 1), (1, 1000), (1000, 1),
                     # ... or, at offset 0, aligned input rows and misaligned
                     # output rows (cached stores)
                     (1027, 2048), (4097, 4096),
-                    # at most 8 rows or columns: one thread per index of the
-                    # long side, 1 to 8 values of the short side each
+                    # at most 16 rows or columns: one thread per index of the
+                    # long side, 1 to 16 values of the short side each
                     (1, 1 << 20), (1 << 20, 1), (3, 100003), (100003, 3),
                     (8, 4097), (4097, 8), (7, 9), (9, 7), (2, 2),
                     # ... as float4s when the long side is a multiple of 4
                     # (aligned, offset 0): every short side 2..8, both ways
                     (2, 1000), (3, 4096), (5, 1024), (6, 2048), (7, 4100), (8, 65536),
                     (65536, 8), (4100, 7), (2048, 6), (1024, 5), (4096, 3), (1000, 2),
-                    (4, 4)]
+                    (4, 4),
+                    # short sides 9..16 (float4 at offset 0 where the long side
+                    # is a multiple of 4)
+                    (16, 65536), (65536, 16), (12, 4100), (9, 4096), (13, 100003),
+                    (4097, 16), (11, 11)]
 
 
 @pytest.mark.parametrize("shape", TRANSPOSE_SHAPES)
