@@ -43,6 +43,14 @@ def _inputs(device):
         "q": mk(1, 4, 256, 128, dtype=torch.float16),
         "k": mk(1, 4, 256, 128, dtype=torch.float16),
         "v": mk(1, 4, 256, 128, dtype=torch.float16),
+        # rows split over workgroups (partials in the workspace)
+        "sl": mk(3, 50001) * 3, "rl": mk(2, 40000), "wl": mk(40000).abs() + 0.5,
+        # head dim 96 on the fast path (dims past 96 zero); head dim 99 on the
+        # register-staged kernel
+        "q96": mk(1, 4, 256, 96, dtype=torch.float16),
+        "k96": mk(1, 4, 256, 96, dtype=torch.float16),
+        "v96": mk(1, 4, 256, 96, dtype=torch.float16),
+        "q99": mk(1, 4, 256, 99), "k99": mk(1, 4, 256, 99), "v99": mk(1, 4, 256, 99),
     }
 
 
@@ -63,9 +71,13 @@ def _all_ops(ops, t):
         ops.gemm(t["a16"], t["b1"][:, :1024].contiguous()),
         ops.gemm(t["a12"], t["b32"]),    # same, fp32
         ops.attention(t["q"], t["k"], t["v"], True),
-        # fp32, 8 query blocks: keys split over workgroups, partials in the
-        # workspace, then the combine kernel
-        ops.attention(t["q"].float(), t["k"].float(), t["v"].float(), False),
+        ops.attention(t["q96"], t["k96"], t["v96"], False),
+        # fp32 head dim 99 (register-staged), 8 query blocks: keys split over
+        # workgroups, partials in the workspace, then the combine kernel
+        ops.attention(t["q99"], t["k99"], t["v99"], False),
+        ops.softmax(t["sl"]),
+        ops.softmax(t["sl"].half()),
+        ops.rmsnorm(t["rl"], t["wl"], 1e-6),
     ]
 
 
@@ -129,3 +141,8 @@ def test_eager_results_match_oracle_spot_check(ops, device):
     r = ops.reduce_sum(t["x"]).item()
     ref = oracle.reduce_sum(t["x"].cpu().numpy())
     assert abs(r - ref) <= 1e-5 * max(abs(ref), 1.0)
+    y = ops.softmax(t["sl"]).cpu().numpy()
+    assert np.max(np.abs(y - oracle.softmax(t["sl"].cpu().numpy()))) <= 1e-6
+    y = ops.rmsnorm(t["rl"], t["wl"], 1e-6).cpu().numpy().astype(np.float64)
+    ref = oracle.rmsnorm(t["rl"].cpu().numpy(), t["wl"].cpu().numpy(), 1e-6)
+    assert np.max(np.abs(y - ref) / np.maximum(np.abs(ref), 1e-30)) <= 1e-5
