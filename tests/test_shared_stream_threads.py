@@ -12,10 +12,12 @@ library together):
     split over workgroups, partials, then the combine kernel);
   * gemm_f16 4352 x 4096 x 512 (272 tiles of 256 x 256: the last round's 16
     tiles are split along K, partial tiles, then the tail sum).
+  * softmax_f32 3 x 50001 (rows split over workgroups: per-segment
+    partials, then the pass that combines them).
 All of them take their scratch from the GPU's arena, which every stream
 shares: the arena's event chain must order the two threads' sequences.
 Each thread has its own inputs and its own output for every call, and
-enqueues 50 rounds of the five calls on ONE shared stream: an explicit
+enqueues 50 rounds of the six calls on ONE shared stream: an explicit
 stream, the null stream, and hipStreamPerThread (where the two threads'
 streams differ although the handle is the same). Every output must match
 the oracle to the tolerances of test_gpu_ops.py, and repeated calls must
@@ -58,6 +60,8 @@ TAIL_N = 4096
 # through scratch (chunk-multiple dims on aligned tensors take the
 # direct-to-LDS kernel, which needs none)
 ATTN_D = 99
+# softmax rows split over workgroups: per-segment partials in scratch
+SPLIT_ROWS = (3, 50001)
 TAIL_ROWS = np.array(sorted({r for t in range(0, TAIL_MK[0], 256) for r in (t, t + 255)}),
                      dtype=np.int32)
 
@@ -74,6 +78,7 @@ class Case:
         self.q, self.k, self.v = (oracle.normal(seed + 5 + i, (1, 4, 256, ATTN_D)) for i in range(3))
         self.at = oracle.to_f16_bits(oracle.uniform(seed + 8, TAIL_MK))
         self.bt = oracle.to_f16_bits(oracle.uniform(seed + 9, (TAIL_MK[1], TAIL_N)))
+        self.sm = oracle.normal(seed + 10, SPLIT_ROWS, 0.0, 3.0)
         f = oracle.from_f16_bits
         self.ref = {
             "reduce": oracle.reduce_sum(self.x),
@@ -81,15 +86,17 @@ class Case:
             "split_k": oracle.gemm(f(self.ap), f(self.bp)),
             "attn": oracle.attention(self.q, self.k, self.v, False),
             "tail": oracle.gemm(f(self.at), f(self.bt), TAIL_ROWS),
+            "softmax": oracle.softmax(self.sm),
         }
         self.dev = {name: to_device(getattr(self, name))
-                    for name in ("x", "a1", "b1", "ap", "bp", "q", "k", "v", "at", "bt")}
+                    for name in ("x", "a1", "b1", "ap", "bp", "q", "k", "v", "at", "bt", "sm")}
         self.out = {
             "reduce": torch.full((rounds,), float("nan"), device="cuda"),
             "skinny": torch.full((rounds, 1, SKINNY_N), float("nan"), device="cuda"),
             "split_k": torch.full((rounds, 1000, 1000), float("nan"), device="cuda"),
             "attn": torch.full((rounds, 1, 4, 256, ATTN_D), float("nan"), device="cuda"),
             "tail": torch.full((rounds, TAIL_MK[0], TAIL_N), float("nan"), device="cuda"),
+            "softmax": torch.full((rounds, *SPLIT_ROWS), float("nan"), device="cuda"),
         }
 
     def enqueue(self, lib, stream, r: int) -> None:
@@ -106,9 +113,11 @@ class Case:
         check(lib.operatorlib_gemm_f16(ptr(d["at"]), ptr(d["bt"]), ptr(o["tail"][r]),
                                        TAIL_MK[0], TAIL_N, TAIL_MK[1], stream),
               "gemm_f16 split tail")
+        check(lib.operatorlib_softmax_f32(ptr(d["sm"]), ptr(o["softmax"][r]), *SPLIT_ROWS,
+                                          stream), "softmax split rows")
 
     def workspace_bytes(self, lib) -> int:
-        """The largest workspace query of the five calls."""
+        """The largest workspace query of the six calls."""
         d = self.dev
         tmp = torch.empty(TAIL_MK[0] * TAIL_N, device="cuda")
         return max(
@@ -120,10 +129,11 @@ class Case:
             lib.operatorlib_attention_f32_workspace_size(ptr(d["q"]), ptr(d["k"]), ptr(d["v"]),
                                                          ptr(tmp), 1, 4, 256, ATTN_D, 0),
             lib.operatorlib_gemm_f16_workspace_size(ptr(d["at"]), ptr(d["bt"]), TAIL_MK[0],
-                                                    TAIL_N, TAIL_MK[1]))
+                                                    TAIL_N, TAIL_MK[1]),
+            lib.operatorlib_softmax_f32_workspace_size(*SPLIT_ROWS))
 
     def enqueue_ws(self, lib, stream, r: int, ws: torch.Tensor) -> None:
-        """The five calls through the *_ws entry points, one after another
+        """The six calls through the *_ws entry points, one after another
         on `stream` in one workspace."""
         d, o = self.dev, self.out
         w, nb = ptr(ws), ws.numel()
@@ -139,6 +149,8 @@ class Case:
         check(lib.operatorlib_gemm_f16_ws(ptr(d["at"]), ptr(d["bt"]), ptr(o["tail"][r]),
                                           TAIL_MK[0], TAIL_N, TAIL_MK[1], w, nb, stream),
               "gemm_f16_ws split tail")
+        check(lib.operatorlib_softmax_f32_ws(ptr(d["sm"]), ptr(o["softmax"][r]), *SPLIT_ROWS,
+                                             w, nb, stream), "softmax_ws split rows")
 
     def verify(self, label: str, rounds=None) -> None:
         rounds = range(self.out["reduce"].numel()) if rounds is None else rounds
@@ -146,6 +158,7 @@ class Case:
         sk = self.out["skinny"].cpu().numpy().astype(np.float64)
         pd = self.out["split_k"].cpu().numpy().astype(np.float64)
         at = self.out["attn"].cpu().numpy().astype(np.float64)
+        smx = self.out["softmax"].cpu().numpy().astype(np.float64)
         ref = self.ref
         for r in rounds:
             where = f"{label} round {r}"
@@ -154,6 +167,8 @@ class Case:
             assert np.max(np.abs(pd[r] - ref["split_k"])) <= 2e-3, where
             err = np.abs(at[r] - ref["attn"])
             assert np.all(err <= 1e-4 + 1e-4 * np.abs(ref["attn"])), where
+            assert np.max(np.abs(smx[r] - ref["softmax"])) <= 1e-6, where
+            assert np.array_equal(smx[r], smx[rounds[0]]), where
             # deterministic: every round gives the first round's bits
             assert red[r] == red[rounds[0]], where
             assert np.array_equal(sk[r], sk[rounds[0]]), where
@@ -306,12 +321,12 @@ def test_capture_workspace_entry_points_overlap_eager_calls(lib, cases):
 
 GRAPHS = 20
 # Device memory the runtime itself may take for 20 instantiated graphs of
-# five calls each (graph objects, kernel arguments); the library adds none.
+# six calls each (graph objects, kernel arguments); the library adds none.
 GRAPH_MEMORY_SLACK = 32 << 20
 
 
 def test_twenty_graphs_hold_no_library_memory(lib, cases):
-    """Capturing the five arena-using calls into 20 graphs leaves library-held
+    """Capturing the six arena-using calls into 20 graphs leaves library-held
     device memory where it was (the arena is static), and every replay gives
     the eager result's bits."""
     _reset(cases)
